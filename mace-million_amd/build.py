@@ -1,0 +1,78 @@
+"""Build step of the MI355X library: generate the architecture-specific kernels and compile everything for gfx950.
+
+    python mace-million_amd/build.py            (also called by __graft_entry__.build())
+
+Output: mace-million_amd/lib/libmace_million_amd.so (git-ignored; it travels with the tree to the GPU box).
+Every HIP source is compiled with -Xclang -target-feature -Xclang -packed-fp32-ops (no packed-FP32 instructions)
+and -munsafe-fp-atomics (hardware float atomics instead of compare-and-swap loops).
+"""
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+GEN = os.path.join(CSRC, "gen")
+OBJ = os.path.join(HERE, "_build")
+LIB_DIR = os.path.join(HERE, "lib")
+LIB = os.path.join(LIB_DIR, "libmace_million_amd.so")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "-munsafe-fp-atomics", "-Wno-unused-command-line-argument"]
+
+
+def generate():
+    sys.path.insert(0, HERE)
+    from mace_onegpu import codegen, model
+
+    return codegen.generate(GEN, model.Tables(model.MaceSpec()))
+
+
+def sources():
+    out = []
+    for d in (CSRC, GEN):
+        for f in sorted(os.listdir(d)):
+            if f.endswith((".hip", ".cpp")):
+                out.append(os.path.join(d, f))
+    return out
+
+
+# files whose fp64 results must be bit-identical to the reference's separately rounded CPU arithmetic
+EXTRA = {"nlist.hip": ["-ffp-contract=off"]}
+
+
+def _compile(src):
+    obj = os.path.join(OBJ, os.path.relpath(src, CSRC).replace(os.sep, "__") + ".o")
+    cmd = [HIPCC] + FLAGS + EXTRA.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def build(jobs=None, verbose=True):
+    generate()
+    os.makedirs(OBJ, exist_ok=True)
+    os.makedirs(LIB_DIR, exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with ThreadPoolExecutor(jobs) as ex:
+        objs = list(ex.map(_compile, srcs))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    shutil.rmtree(OBJ, ignore_errors=True)
+    if verbose:
+        print(f"built {LIB} from {len(srcs)} sources")
+    return LIB
+
+
+if __name__ == "__main__":
+    build()

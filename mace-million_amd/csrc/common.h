@@ -1,0 +1,44 @@
+// Shared definitions of the MI355X (gfx950) three-pass MACE library.
+//
+// Conventions of every extern "C" entry point (declared in include/mace_million_amd.h):
+//   * returns 0 on success, a negative MM_E* code on failure; mm_last_error() gives the text of the last failure
+//     of the calling thread;
+//   * takes device pointers, element counts and a hipStream_t; launches work on that stream; never allocates,
+//     never frees, never synchronises (so every entry point can be captured into a hipGraph);
+//   * all buffers belong to the caller.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#define MM_OK 0
+#define MM_EINVAL -1
+#define MM_ELAUNCH -2
+#define MM_ERANGE -3
+
+namespace mm {
+void set_error(const std::string& msg);
+int launch_status(const char* what);   // hipGetLastError() -> status code (records the message)
+}  // namespace mm
+
+#define MM_CHECK_ARG(cond, msg)                 \
+  do {                                          \
+    if (!(cond)) {                              \
+      mm::set_error(std::string(__func__) + ": " + (msg)); \
+      return MM_EINVAL;                         \
+    }                                           \
+  } while (0)
+
+// channel count of the model (128 for the MACE-MPA-0 architecture); the generated kernels assume it
+#define MM_C 128
+// channel blocks: one per XCD of the MI355X (8 XCDs); a block of CB channels stays on one XCD's L2
+#define MM_NCB 8
+#define MM_CB 16
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int mm_xcd_channel_block() {
+  // workgroups are dispatched round-robin over the 8 XCDs: blockIdx.x % 8 selects the XCD, and with it the
+  // channel block whose table slice that XCD keeps in its L2
+  return blockIdx.x & (MM_NCB - 1);
+}

@@ -1,0 +1,225 @@
+// Cell-list neighbour build, bit-exact with the reference's System / build_neighbors
+// (receiver_chunk_mace.py:82-165):
+//   wrap      : m = fmod(x, L); m + L where the signs of m and L differ (torch.remainder)
+//   cell      : min(floor(m / (L / ncell)), ncell - 1), ncell = max(1, floor(L / r_max)) (host)
+//   order     : 10-bit Morton code (x -> bit 3b+2, y -> 3b+1, z -> 3b), stable radix sort -> perm
+//   candidates: the 27 cells (c + o) mod ncell for o in (-1, 0, 1)^3, x-offset slowest (meshgrid "ij"), each
+//               cell's atoms in sorted order; all atoms 0..N-1 in order if any ncell < 3
+//   test      : d = v - L * rint(v / L) (half to even, as torch.round), dd = (dx^2 + dy^2) + dz^2, keep
+//               dd < r_max^2 and j != i; candidate order preserved.
+// Every fp64 operation is a separately rounded IEEE operation: the file is compiled with -ffp-contract=off and
+// the arithmetic scopes carry "#pragma clang fp contract(off)" (HIP's __dmul_rn / __dadd_rn are plain * and +,
+// which clang would otherwise fuse into FMAs and so change dd at the last bit).  Output: CSR (rowptr int64 [N+1], senders int32 [E]) in the sorted index space.
+#include "common.h"
+
+#include <hipcub/hipcub.hpp>
+
+__global__ void mm_nl_prepare_kernel(const double* __restrict__ pos_in, long N, double bx, double by, double bz,
+                                     double cx, double cy, double cz, int nx, int ny, int nz,
+                                     double* __restrict__ pos_w, int* __restrict__ cell,
+                                     long long* __restrict__ key, long long* __restrict__ idx) {
+#pragma clang fp contract(off)
+  const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const double L[3] = {bx, by, bz};
+  const double cs[3] = {cx, cy, cz};
+  const int nc[3] = {nx, ny, nz};
+  int c[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    double m = fmod(pos_in[3 * i + k], L[k]);
+    if (m != 0.0 && ((m < 0.0) != (L[k] < 0.0))) m = __dadd_rn(m, L[k]);
+    pos_w[3 * i + k] = m;
+    long q = (long)floor(__ddiv_rn(m, cs[k]));
+    if (q > nc[k] - 1) q = nc[k] - 1;
+    c[k] = (int)q;
+    cell[3 * i + k] = c[k];
+  }
+  long long code = 0;
+#pragma unroll
+  for (int b = 0; b < 10; ++b) {
+    code |= ((long long)((c[0] >> b) & 1)) << (3 * b + 2);
+    code |= ((long long)((c[1] >> b) & 1)) << (3 * b + 1);
+    code |= ((long long)((c[2] >> b) & 1)) << (3 * b);
+  }
+  key[i] = code;
+  idx[i] = i;
+}
+
+__global__ void mm_nl_gather_kernel(const long long* __restrict__ perm, long N, const double* __restrict__ pos_w,
+                                    const int* __restrict__ cell, const int* __restrict__ spec_in,
+                                    double* __restrict__ pos_s, int* __restrict__ cell_s, int* __restrict__ spec_s) {
+  const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const long j = perm[i];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    pos_s[3 * i + k] = pos_w[3 * j + k];
+    cell_s[3 * i + k] = cell[3 * j + k];
+  }
+  if (spec_in) spec_s[i] = spec_in[j];
+}
+
+// start[cl] = first sorted atom of cell cl (N if empty), count[cl]; atoms of a cell are contiguous after the sort
+__global__ void mm_nl_ranges_kernel(const int* __restrict__ cell_s, long N, int ny, int nz, int* __restrict__ start,
+                                    int* __restrict__ count) {
+  const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const int cl = (cell_s[3 * i] * ny + cell_s[3 * i + 1]) * nz + cell_s[3 * i + 2];
+  const int prev = i > 0 ? (cell_s[3 * (i - 1)] * ny + cell_s[3 * (i - 1) + 1]) * nz + cell_s[3 * (i - 1) + 2] : -1;
+  const int next = i + 1 < N ? (cell_s[3 * (i + 1)] * ny + cell_s[3 * (i + 1) + 1]) * nz + cell_s[3 * (i + 1) + 2]
+                             : -1;
+  if (cl != prev) start[cl] = (int)i;
+  if (cl != next) count[cl] = (int)(i + 1);   // end, turned into a count below
+}
+
+__global__ void mm_nl_counts_kernel(int ncells, const int* __restrict__ start, int* __restrict__ count, long N) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= ncells) return;
+  count[c] = start[c] < N ? count[c] - start[c] : 0;
+}
+
+__global__ void mm_fill_i32_kernel_nl(int* __restrict__ p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__device__ __forceinline__ double mm_mic(double v, double L) {
+#pragma clang fp contract(off)
+  return __dsub_rn(v, __dmul_rn(L, rint(__ddiv_rn(v, L))));
+}
+
+template <bool FILL>
+__global__ void mm_nl_pairs_kernel(const double* __restrict__ pos, const int* __restrict__ cell, long N, double bx,
+                                   double by, double bz, int nx, int ny, int nz, const int* __restrict__ start,
+                                   const int* __restrict__ count, double r2, int brute, int* __restrict__ NN,
+                                   const long* __restrict__ rowptr, int* __restrict__ send) {
+  const long i = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  const double xi = pos[3 * i], yi = pos[3 * i + 1], zi = pos[3 * i + 2];
+  long n = 0;
+  const long base = FILL ? rowptr[i] : 0;
+  auto test = [&](long j) {
+#pragma clang fp contract(off)
+    const double dx = mm_mic(__dsub_rn(xi, pos[3 * j]), bx);
+    const double dy = mm_mic(__dsub_rn(yi, pos[3 * j + 1]), by);
+    const double dz = mm_mic(__dsub_rn(zi, pos[3 * j + 2]), bz);
+    const double dd = __dadd_rn(__dadd_rn(__dmul_rn(dx, dx), __dmul_rn(dy, dy)), __dmul_rn(dz, dz));
+    if (dd < r2 && j != i) {
+      if (FILL) send[base + n] = (int)j;
+      ++n;
+    }
+  };
+  if (brute) {
+    for (long j = 0; j < N; ++j) test(j);
+  } else {
+    const int cx = cell[3 * i], cy = cell[3 * i + 1], cz = cell[3 * i + 2];
+    for (int ox = -1; ox <= 1; ++ox) {
+      const int ax = ((cx + ox) % nx + nx) % nx;
+      for (int oy = -1; oy <= 1; ++oy) {
+        const int ay = ((cy + oy) % ny + ny) % ny;
+        for (int oz = -1; oz <= 1; ++oz) {
+          const int az = ((cz + oz) % nz + nz) % nz;
+          const int cl = (ax * ny + ay) * nz + az;
+          const int st = start[cl], ct = count[cl];
+          for (int k = 0; k < ct; ++k) test((long)st + k);
+        }
+      }
+    }
+  }
+  if (!FILL) NN[i] = (int)n;
+}
+
+extern "C" int mm_nl_workspace_bytes(long N, size_t* bytes) {
+  MM_CHECK_ARG(N >= 0 && N < (1L << 31) && bytes, "bad sizes");
+  size_t a = 0, b = 0;
+  hipcub::DeviceRadixSort::SortPairs(nullptr, a, (const long long*)nullptr, (long long*)nullptr,
+                                     (const long long*)nullptr, (long long*)nullptr, (int)N, 0, 30);
+  hipcub::DeviceScan::ExclusiveSum(nullptr, b, (const long*)nullptr, (long*)nullptr, (int)N + 1);
+  *bytes = (a > b ? a : b) + 256;
+  return MM_OK;
+}
+
+extern "C" int mm_nl_prepare(const double* pos_in, long N, const double* box, const int* ncell, const double* cs,
+                             double* pos_w, int* cell, long long* key, long long* idx, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && box && ncell && cs, "bad arguments");
+  for (int k = 0; k < 3; ++k) MM_CHECK_ARG(ncell[k] >= 1 && ncell[k] <= 1024, "ncell out of range (10-bit Morton)");
+  if (N == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_nl_prepare_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream, pos_in, N, box[0],
+                     box[1], box[2], cs[0], cs[1], cs[2], ncell[0], ncell[1], ncell[2], pos_w, cell, key, idx);
+  return mm::launch_status("mm_nl_prepare");
+}
+
+extern "C" int mm_nl_sort(const long long* key_in, long long* key_out, const long long* idx_in, long long* perm,
+                          long N, void* ws, size_t ws_bytes, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && N < (1L << 31), "bad sizes");
+  if (N == 0) return MM_OK;
+  size_t need = 0;
+  hipcub::DeviceRadixSort::SortPairs(nullptr, need, key_in, key_out, idx_in, perm, (int)N, 0, 30, stream);
+  MM_CHECK_ARG(ws_bytes >= need, "workspace too small");
+  if (hipcub::DeviceRadixSort::SortPairs(ws, need, key_in, key_out, idx_in, perm, (int)N, 0, 30, stream) !=
+      hipSuccess)
+    return mm::launch_status("mm_nl_sort");
+  return mm::launch_status("mm_nl_sort");
+}
+
+extern "C" int mm_nl_gather(const long long* perm, long N, const double* pos_w, const int* cell, const int* spec_in,
+                            double* pos_s, int* cell_s, int* spec_s, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0, "bad sizes");
+  if (N == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_nl_gather_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream, perm, N, pos_w, cell,
+                     spec_in, pos_s, cell_s, spec_s);
+  return mm::launch_status("mm_nl_gather");
+}
+
+extern "C" int mm_nl_cell_ranges(const int* cell_s, long N, const int* ncell, int* start, int* count,
+                                 hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && ncell, "bad arguments");
+  const int ncells = ncell[0] * ncell[1] * ncell[2];
+  hipLaunchKernelGGL(mm_fill_i32_kernel_nl, dim3((ncells + 255) / 256), dim3(256), 0, stream, start, ncells, (int)N);
+  hipLaunchKernelGGL(mm_fill_i32_kernel_nl, dim3((ncells + 255) / 256), dim3(256), 0, stream, count, ncells, 0);
+  if (N > 0)
+    hipLaunchKernelGGL(mm_nl_ranges_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, stream, cell_s, N,
+                       ncell[1], ncell[2], start, count);
+  hipLaunchKernelGGL(mm_nl_counts_kernel, dim3((ncells + 255) / 256), dim3(256), 0, stream, ncells, start, count, N);
+  return mm::launch_status("mm_nl_cell_ranges");
+}
+
+extern "C" int mm_nl_count(const double* pos_s, const int* cell_s, long N, const double* box, const int* ncell,
+                           const int* start, const int* count, double r2, int brute, int* NN, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && box && ncell, "bad arguments");
+  if (N == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_nl_pairs_kernel<false>, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, stream, pos_s,
+                     cell_s, N, box[0], box[1], box[2], ncell[0], ncell[1], ncell[2], start, count, r2, brute, NN,
+                     (const long*)nullptr, (int*)nullptr);
+  return mm::launch_status("mm_nl_count");
+}
+
+extern "C" int mm_nl_scan(const int* NN, long* rowptr, long N, void* ws, size_t ws_bytes, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && N < (1L << 31), "bad sizes");
+  // rowptr[0] = 0, rowptr[i + 1] = sum_{j <= i} NN[j]: exclusive scan of NN widened to int64, over N + 1 items
+  // (the last input item is a zero appended by the widening iterator)
+  struct Widen {
+    const int* p;
+    long n;
+    __host__ __device__ long operator()(const long& i) const { return i < n ? (long)p[i] : 0L; }
+  };
+  hipcub::CountingInputIterator<long> cnt(0);
+  hipcub::TransformInputIterator<long, Widen, hipcub::CountingInputIterator<long>> it(cnt, Widen{NN, N});
+  size_t need = 0;
+  hipcub::DeviceScan::ExclusiveSum(nullptr, need, it, rowptr, (int)N + 1, stream);
+  MM_CHECK_ARG(ws_bytes >= need, "workspace too small");
+  hipcub::DeviceScan::ExclusiveSum(ws, need, it, rowptr, (int)N + 1, stream);
+  return mm::launch_status("mm_nl_scan");
+}
+
+extern "C" int mm_nl_fill(const double* pos_s, const int* cell_s, long N, const double* box, const int* ncell,
+                          const int* start, const int* count, double r2, int brute, const long* rowptr, int* send,
+                          hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && box && ncell, "bad arguments");
+  if (N == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_nl_pairs_kernel<true>, dim3((unsigned)((N + 127) / 128)), dim3(128), 0, stream, pos_s,
+                     cell_s, N, box[0], box[1], box[2], ncell[0], ncell[1], ncell[2], start, count, r2, brute,
+                     (int*)nullptr, rowptr, send);
+  return mm::launch_status("mm_nl_fill");
+}

@@ -1,0 +1,234 @@
+// Node-level small kernels of the three-pass path: buffer fills (graph-capture-safe zeroing), per-species row
+// lists, the two readouts with their gradients and energy accumulation, the periodic-image ghost exchange, and
+// the assembly of per-atom forces from per-pair forces.
+#include "common.h"
+
+#include <math.h>
+
+// ------------------------------------------------------------------------------------------------ fills
+__global__ void mm_fill_f32_kernel(float* p, long n, float v) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = v;
+}
+__global__ void mm_fill_f64_kernel(double* p, long n, double v) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = v;
+}
+__global__ void mm_fill_i32_kernel(int* p, long n, int v) {
+  for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = v;
+}
+
+static dim3 fill_grid(long n) {
+  long b = (n + 255) / 256;
+  if (b > 65536) b = 65536;
+  if (b < 1) b = 1;
+  return dim3((unsigned)b);
+}
+
+extern "C" int mm_fill_f32(float* p, long n, float v, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0, "negative size");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_fill_f32_kernel, fill_grid(n), dim3(256), 0, stream, p, n, v);
+  return mm::launch_status("mm_fill_f32");
+}
+extern "C" int mm_fill_f64(double* p, long n, double v, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0, "negative size");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_fill_f64_kernel, fill_grid(n), dim3(256), 0, stream, p, n, v);
+  return mm::launch_status("mm_fill_f64");
+}
+extern "C" int mm_fill_i32(int* p, long n, int v, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0, "negative size");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_fill_i32_kernel, fill_grid(n), dim3(256), 0, stream, p, n, v);
+  return mm::launch_status("mm_fill_i32");
+}
+
+// ------------------------------------------------------------------------------------------------ species lists
+// Stable partition of rows 0..n-1 by species: lists[s * stride + j] = j-th row of species s, counts[s].
+// One workgroup of 1024 threads; thread t owns a contiguous segment of rows.
+#define MM_MAX_SPECIES 16
+__global__ void __launch_bounds__(1024) mm_species_lists_kernel(const int* __restrict__ spec, int n, int S,
+                                                                int* __restrict__ lists, long stride,
+                                                                int* __restrict__ counts) {
+  __shared__ int cnt[MM_MAX_SPECIES][1024];
+  const int t = threadIdx.x;
+  const int per = (n + 1023) / 1024;
+  const int b = t * per, e = min(n, b + per);
+  int local[MM_MAX_SPECIES];
+  for (int s = 0; s < S; ++s) local[s] = 0;
+  for (int j = b; j < e; ++j) local[spec[j]]++;
+  for (int s = 0; s < S; ++s) cnt[s][t] = local[s];
+  __syncthreads();
+  // exclusive scan per species over the 1024 thread counts (Hillis-Steele in place on a copy)
+  for (int s = 0; s < S; ++s) {
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int v = t >= off ? cnt[s][t - off] : 0;
+      __syncthreads();
+      cnt[s][t] += v;
+      __syncthreads();
+    }
+  }
+  int pos[MM_MAX_SPECIES];
+  for (int s = 0; s < S; ++s) pos[s] = cnt[s][t] - local[s];
+  for (int j = b; j < e; ++j) {
+    const int s = spec[j];
+    lists[(size_t)s * stride + pos[s]++] = j;
+  }
+  if (t == 1023)
+    for (int s = 0; s < S; ++s) counts[s] = cnt[s][1023];
+}
+
+extern "C" int mm_species_lists(const int* spec, int n, int S, int* lists, long stride, int* counts,
+                                hipStream_t stream) {
+  MM_CHECK_ARG(S >= 1 && S <= MM_MAX_SPECIES && n >= 0 && stride >= n, "bad sizes");
+  hipLaunchKernelGGL(mm_species_lists_kernel, dim3(1), dim3(1024), 0, stream, spec, n, S, lists, stride, counts);
+  return mm::launch_status("mm_species_lists");
+}
+
+// ------------------------------------------------------------------------------------------------ readouts
+// R1(h1) = h1[0e] . w0 (w0 = r0 / sqrt(C)); in pass C: eat[i] += scale R1_i and
+// g_h1[i] = G1r[i] + scale dR1/dh1 (the loss of pass C is scale sum R1 + sum G1r . h1, mliap_threepass.py:579).
+// One wave per node.
+__global__ void mm_readout1_kernel(int n, const float* __restrict__ h1, long h_stride, const float* __restrict__ w0,
+                                   float scale, double* __restrict__ eat, const float* __restrict__ g1r,
+                                   long g1_stride, float* __restrict__ gh, long gh_stride, int D) {
+  const int node = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (node >= n) return;
+  const int lane = threadIdx.x & 63;
+  const float* __restrict__ hp = h1 + (size_t)node * h_stride;
+  float s = hp[lane] * w0[lane] + hp[lane + 64] * w0[lane + 64];
+  for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) eat[node] += (double)(scale * s);
+  if (gh) {
+    const float* __restrict__ gp = g1r + (size_t)node * g1_stride;
+    float* __restrict__ op = gh + (size_t)node * gh_stride;
+    for (int j = lane; j < D; j += 64) op[j] = gp[j] + (j < MM_C ? scale * w0[j] : 0.f);
+  }
+}
+
+extern "C" int mm_readout1(int n, const float* h1, long h_stride, const float* w0, float scale, double* eat,
+                           const float* g1r, long g1_stride, float* gh, long gh_stride, int D, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0 && D >= MM_C, "bad sizes");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_readout1_kernel, dim3((n + 3) / 4), dim3(256), 0, stream, n, h1, h_stride, w0, scale, eat,
+                     g1r, g1_stride, gh, gh_stride, D);
+  return mm::launch_status("mm_readout1");
+}
+
+// R2(h2) = sum_j w2_j silu_n(h2 . W1[:, j]) with W1 = r1_w1 / sqrt(C), w2 = r1_w2 / sqrt(16), silu_n = cst silu;
+// eat[i] += scale R2_i;  g_h2[i] = scale dR2/dh2.  One wave per node, hidden width H <= 64.
+__global__ void mm_readout2_kernel(int n, const float* __restrict__ h2, long h_stride, const float* __restrict__ W1,
+                                   const float* __restrict__ w2, int H, float cst, float scale,
+                                   double* __restrict__ eat, float* __restrict__ gh, long gh_stride) {
+  const int node = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (node >= n) return;
+  const int lane = threadIdx.x & 63;
+  const float* __restrict__ hp = h2 + (size_t)node * h_stride;
+  const float a0 = hp[lane], a1 = hp[lane + 64];
+  float e = 0.f, g0 = 0.f, g1 = 0.f;
+  for (int j = 0; j < H; ++j) {
+    const float wa = W1[lane * H + j], wb = W1[(lane + 64) * H + j];
+    float z = a0 * wa + a1 * wb;
+    for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o);   // every lane holds the full z_j
+    const float sg = 1.f / (1.f + expf(-z));
+    e += w2[j] * cst * z * sg;
+    const float gz = scale * w2[j] * cst * sg * (1.f + z * (1.f - sg));   // scale * d/dz (w2_j cst silu(z))
+    g0 = fmaf(gz, wa, g0);
+    g1 = fmaf(gz, wb, g1);
+  }
+  if (lane == 0) eat[node] += (double)(scale * e);
+  float* __restrict__ op = gh + (size_t)node * gh_stride;
+  op[lane] = g0;
+  op[lane + 64] = g1;
+}
+
+extern "C" int mm_readout2(int n, const float* h2, long h_stride, const float* W1, const float* w2, int H,
+                           float cst, float scale, double* eat, float* gh, long gh_stride, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0 && H >= 1 && H <= 64, "bad sizes");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_readout2_kernel, dim3((n + 3) / 4), dim3(256), 0, stream, n, h2, h_stride, W1, w2, H, cst,
+                     scale, eat, gh, gh_stride);
+  return mm::launch_status("mm_readout2");
+}
+
+// ------------------------------------------------------------------------------------------------ ghost exchange
+// Periodic images stand in for LAMMPS' ghost atoms on one GPU: ghost g (row nlocal + g) is a copy of owner[g].
+// forward: dst[0:nlocal] = src[0:nlocal]; dst[nlocal + g] = src[owner[g]]     (data.forward_exchange)
+// reverse: dst[o] = src[o] + sum_{ghosts g of o} src[nlocal + g]               (data.reverse_exchange)
+// The reverse sum walks an owner-sorted CSR of the ghosts (deterministic, no atomics).
+__global__ void mm_ghost_forward_kernel(const float* __restrict__ src, float* __restrict__ dst, int D, int nlocal,
+                                        int nghost, const int* __restrict__ owner) {
+  const long row = blockIdx.y * (long)gridDim.x + blockIdx.x;
+  if (row >= (long)nlocal + nghost) return;
+  const long from = row < nlocal ? row : (long)owner[row - nlocal];
+  for (int j = threadIdx.x; j < D; j += blockDim.x) dst[row * D + j] = src[from * D + j];
+}
+
+__global__ void mm_ghost_reverse_kernel(const float* __restrict__ src, float* __restrict__ dst, int D, int nlocal,
+                                        const int* __restrict__ g_rowptr, const int* __restrict__ g_list) {
+  const long row = blockIdx.y * (long)gridDim.x + blockIdx.x;
+  if (row >= nlocal) return;
+  const int b = g_rowptr[row], e = g_rowptr[row + 1];
+  for (int j = threadIdx.x; j < D; j += blockDim.x) {
+    float s = src[row * D + j];
+    for (int k = b; k < e; ++k) s += src[((long)nlocal + g_list[k]) * D + j];
+    dst[row * D + j] = s;
+  }
+}
+
+static dim3 rows_grid(long rows) {
+  const long gx = rows < 65535 ? (rows > 0 ? rows : 1) : 65535;
+  return dim3((unsigned)gx, (unsigned)((rows + gx - 1) / gx));
+}
+
+extern "C" int mm_ghost_forward(const float* src, float* dst, int D, int nlocal, int nghost, const int* owner,
+                                hipStream_t stream) {
+  MM_CHECK_ARG(D >= 1 && nlocal >= 0 && nghost >= 0, "bad sizes");
+  if (nlocal + nghost == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_ghost_forward_kernel, rows_grid((long)nlocal + nghost), dim3(128), 0, stream, src, dst, D,
+                     nlocal, nghost, owner);
+  return mm::launch_status("mm_ghost_forward");
+}
+
+extern "C" int mm_ghost_reverse(const float* src, float* dst, int D, int nlocal, const int* g_rowptr,
+                                const int* g_list, hipStream_t stream) {
+  MM_CHECK_ARG(D >= 1 && nlocal >= 0, "bad sizes");
+  if (nlocal == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_ghost_reverse_kernel, rows_grid(nlocal), dim3(128), 0, stream, src, dst, D, nlocal, g_rowptr,
+                     g_list);
+  return mm::launch_status("mm_ghost_reverse");
+}
+
+// ------------------------------------------------------------------------------------------------ forces
+// F[i] = - sum_{e in row(i)} PF_e + sum_{e : send(e) = i} PF_e with v_e = x_recv - x_send (the reference's
+// _accum_forces, receiver_chunk_mace.py:272-276).  Receiver part: CSR over the receiver-sorted pairs; sender
+// part: CSR over the pairs sorted by sender (s_perm lists pair ids per sender).  fp64 accumulation.
+__global__ void mm_pair_forces_to_atoms_kernel(int n, const long* __restrict__ rowptr, const long* __restrict__ s_rowptr,
+                                               const long* __restrict__ s_perm, const float* __restrict__ pf,
+                                               double* __restrict__ F) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  double fx = 0, fy = 0, fz = 0;
+  for (long e = rowptr[i]; e < rowptr[i + 1]; ++e) {
+    fx -= pf[3 * e];
+    fy -= pf[3 * e + 1];
+    fz -= pf[3 * e + 2];
+  }
+  for (long k = s_rowptr[i]; k < s_rowptr[i + 1]; ++k) {
+    const long e = s_perm[k];
+    fx += pf[3 * e];
+    fy += pf[3 * e + 1];
+    fz += pf[3 * e + 2];
+  }
+  F[3 * (size_t)i] = fx;
+  F[3 * (size_t)i + 1] = fy;
+  F[3 * (size_t)i + 2] = fz;
+}
+
+extern "C" int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* s_rowptr, const long* s_perm,
+                                       const float* pf, double* F, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0, "bad sizes");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_pair_forces_to_atoms_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, n, rowptr,
+                     s_rowptr, s_perm, pf, F);
+  return mm::launch_status("mm_pair_forces_to_atoms");
+}

@@ -1,0 +1,12 @@
+"""MI355X-native receiver-chunked three-pass MACE energy + forces.
+
+Module map (mirrors the reference package mace_onegpu, same module paths for the drop-in API):
+  mliap_threepass   ThreePassMLIAP: LAMMPS ML-IAP unified plugin, compute_forces(data)
+  fused_conv        FusedConvTP: channelwise TP + receiver scatter as an nn.Module
+  receiver_chunk_mace  System (GPU cell-list neighbours), ReceiverChunkMACE (standalone three-pass)
+  graphed_three_pass   GraphedThreePass: HIP-graph replay of full chunks, velocity-Verlet MD driver
+  fast_layers       per-chunk layer pipelines on the HIP kernels
+  lammps_data       periodic-image ML-IAP data object (one GPU stands in for LAMMPS' ghost exchange)
+  model, o3, codegen, systems, _lib   architecture, couplings, kernel generator, inputs, C-ABI binding
+"""
+__version__ = "0.1.0"

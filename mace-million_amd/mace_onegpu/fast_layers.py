@@ -1,0 +1,304 @@
+"""Per-chunk layer pipelines of the three-pass evaluation on the MI355X kernels.
+
+Mirrors the reference's FastLayers (fast_layers.py:108-222): the exact node-level speed-ups (species-block
+skip_tp, receiver-only node operations, tabulated radial weights) and the layer functions used by the three passes.
+Here every pass is an explicit sequence of HIP kernels with a hand-derived backward (no autograd):
+
+  layer 1 (pass A, and pass C with its backward):
+    geometry -> conv1 (spline W x TP x receiver sum, density) -> [linear o skip_tp] per species / (rho + 1)
+    -> symmetric contraction -> product linear -> (pass C) readout 1 and g_h1 = scale dR1/dh1 + G1r
+    -> backward through the same chain -> per-edge dL/dv
+  layer 2 (pass B):
+    skip_tp(h1) per species, linear_up(H1[nodes]) -> conv2 -> linear / (rho + 1) -> symmetric contraction
+    -> product linear + sc -> readout 2 -> backward -> per-edge dL/dv, G1[nodes] += dL/dh1
+
+linear and skip_tp of layer 1 are both linear per (l, species) and act back to back, so they are applied as one
+128x128 block per (l, species) (W_lin_l @ W_skip_l,s); the result is the same map.
+"""
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from . import codegen, model as mm
+from ._lib import K, stream
+
+C = 128
+NCB = 8
+SRC = 3                         # max K-chunks of one linear output component (mm_linear)
+
+
+def mfma_block(W):
+    """[128, 128] (k, n) -> flat float32 in the B-operand lane order of mm_linear: index ((t*128+n)*4+g)*4+u."""
+    W = W.reshape(8, 4, 4, 128)               # [t, g, u, n]
+    return W.permute(0, 3, 1, 2).reshape(-1).contiguous()
+
+
+def host_ints(vals):
+    arr = (ctypes.c_int * len(vals))(*vals)
+    return arr
+
+
+class LinPlan:
+    """Component table of one mm_linear launch."""
+
+    def __init__(self, comps):
+        # comps: list of (out_off, [(in_off, w_idx), ...])
+        self.n = len(comps)
+        nsrc, inoff, widx, outoff = [], [], [], []
+        for out_off, srcs in comps:
+            assert 1 <= len(srcs) <= SRC
+            nsrc.append(len(srcs))
+            for q in range(SRC):
+                io, wi = srcs[q] if q < len(srcs) else (0, 0)
+                inoff.append(io)
+                widx.append(wi)
+            outoff.append(out_off)
+        self.nsrc, self.inoff = host_ints(nsrc), host_ints(inoff)
+        self.widx, self.outoff = host_ints(widx), host_ints(outoff)
+
+
+def comp_of(ls):
+    out, o = [], 0
+    for l in ls:
+        out.append(o)
+        o += 2 * l + 1
+    return out, o
+
+
+class FastLayers:
+    """Device constants of the model for a set of present species (model element columns) and the layer pipelines.
+
+    species_cols: sorted model element indices present in the system (the reference's `cols`,
+    mliap_threepass.py:217); spline_grid: knots M of the radial-weight tables (reference default 512)."""
+
+    def __init__(self, model, species_cols, spline_grid=512, r_lo=0.5, device="cuda"):
+        self.dev = torch.device(device)
+        sp = model.spec
+        self.spec = sp
+        self.cols = [int(c) for c in species_cols]
+        S = len(self.cols)
+        self.S = S
+        ne = sp.num_elements
+        P = {k: v.detach().to("cpu", torch.float64) for k, v in model.p.items()}
+        self.tables = model.tables
+        dev = self.dev
+        f32 = dict(dtype=torch.float32, device=dev)
+        col2s = torch.full((ne,), -1, dtype=torch.int32)
+        col2s[torch.as_tensor(self.cols)] = torch.arange(S, dtype=torch.int32)
+        self.col2s = col2s.to(dev)
+        # -------- layer 1 node features per species: linear_up(node_embedding(onehot))
+        emb = P["emb"][self.cols] / math.sqrt(ne)
+        self.Xs1 = (emb @ P["i0_up"][0] / math.sqrt(C)).to(**f32).contiguous()
+        # -------- GEMM weight blocks
+        def blocks(mats):
+            return torch.cat([mfma_block(m.to(torch.float32)) for m in mats]).to(dev)
+        comb = [P["i0_lin"][l] / math.sqrt(C) @ (P["i0_skip"][l][:, c, :] / math.sqrt(C * ne))
+                for c in self.cols for l in range(4)]                                   # block s*4 + l
+        self.W_l1 = blocks(comb)
+        self.W_l1T = blocks([m.T for m in comb])
+        pl1 = [P["p0_lin"][l] / math.sqrt(C) for l in range(2)]
+        self.W_p1, self.W_p1T = blocks(pl1), blocks([m.T for m in pl1])
+        up2 = [P["i1_up"][l] / math.sqrt(C) for l in range(2)]
+        self.W_up2, self.W_up2T = blocks(up2), blocks([m.T for m in up2])
+        sk1 = [P["i1_skip"][:, c, :] / math.sqrt(C * ne) for c in self.cols]
+        self.W_sk1, self.W_sk1T = blocks(sk1), blocks([m.T for m in sk1])
+        src = self.tables.lin2_src
+        lin2, self.lin2_block = [], {}
+        for l in range(4):
+            for j, w in enumerate(src[l]):
+                self.lin2_block[(l, w)] = len(lin2)
+                lin2.append(P[f"i1_lin_l{l}"][j] / math.sqrt(C * len(src[l])))
+        self.W_lin2, self.W_lin2T = blocks(lin2), blocks([m.T for m in lin2])
+        pl2 = [P["p1_lin"][0] / math.sqrt(C)]
+        self.W_p2, self.W_p2T = blocks(pl2), blocks([m.T for m in pl2])
+        # -------- symmetric contraction weights [S, paths, C] in the generated kernels' order
+        def symc_w(k, paths, out_ls):
+            rows = []
+            for (L, nu, pth) in codegen.symc_path_order(paths, out_ls):
+                j = paths[L][nu].index(pth)
+                rows.append(P[f"p{k}_w_L{L}_nu{nu}"][:, j, :])                     # [ne, C]
+            return torch.stack(rows, 1)[self.cols].to(**f32).contiguous()
+        self.Wsc1 = symc_w(0, self.tables.sc1, [0, 1])
+        self.Wsc2 = symc_w(1, self.tables.sc2, [0])
+        # -------- readouts, density, energy constants
+        self.r0s = (P["r0"] / math.sqrt(C)).to(**f32).contiguous()
+        self.r1W1 = (P["r1_w1"] / math.sqrt(C)).to(**f32).contiguous()
+        self.r1w2 = (P["r1_w2"] / math.sqrt(P["r1_w2"].shape[0])).to(**f32).contiguous()
+        self.H_ro = P["r1_w2"].shape[0]
+        self.dens = [(ctypes.c_float * sp.num_bessel)(*(P[f"i{k}_dens"][:, 0] / math.sqrt(sp.num_bessel)).tolist())
+                     for k in range(2)]
+        self.scale, self.shift = sp.scale, sp.shift
+        self.e0 = model.e0.detach().to(dev, torch.float64)
+        # -------- spline tables (fp64 sampling on the GPU)
+        self.M, self.r_lo, self.r_hi = int(spline_grid), float(r_lo), sp.r_max
+        self.h = (self.r_hi - self.r_lo) / (self.M - 1)
+        self.inv_h = 1.0 / self.h
+        # the radial embedding of this architecture has no species-dependent distance transform: every ordered
+        # pair has the same W(r), so one table serves all pairs (pair_map -> 0)
+        self.n_tab = 1
+        self.pair_map = torch.zeros(S * S, dtype=torch.int32, device=dev)
+        self.tab = [self._build_table(P, k) for k in range(2)]
+        # -------- linear plans
+        o1, _ = comp_of([0, 1, 2, 3])
+        self.plan_l1 = LinPlan([((o1[l] + m) * C, [((o1[l] + m) * C, l)]) for l in range(4) for m in range(2 * l + 1)])
+        self.plan_p1 = LinPlan([(j * C, [(j * C, 0 if j == 0 else 1)]) for j in range(4)])
+        self.plan_sk1 = LinPlan([(0, [(0, 0)])])
+        self.plan_p2 = LinPlan([(0, [(0, 0)])])
+        mo, _ = comp_of(self.tables.tp2["mid_ls"])
+        mid_ls = self.tables.tp2["mid_ls"]
+        self.plan_lin2 = LinPlan([((o1[l] + m) * C, [((mo[w] + m) * C, self.lin2_block[(l, w)]) for w in src[l]])
+                                  for l in range(4) for m in range(2 * l + 1)])
+        self.plan_lin2T = LinPlan([((mo[w] + m) * C, [((o1[mid_ls[w]] + m) * C, self.lin2_block[(mid_ls[w], w)])])
+                                   for w in range(len(mid_ls)) for m in range(2 * mid_ls[w] + 1)])
+        self.nO1, self.nO2 = self.tables.tp1["nO"], self.tables.tp2["nO"]
+        self.ws = None
+
+    # ------------------------------------------------------------------ tables
+    def _build_table(self, P, k):
+        """conv_spline.build_tables / spline_radial._sample on the GPU in fp64, then per-interval coefficients."""
+        dev = self.dev
+        Ws = [P[f"i{k}_r{j}"].to(dev).contiguous() for j in range(4)]
+        nW = self.tables.tp1["nW"] if k == 0 else self.tables.tp2["nW"]
+        D = nW * C
+        M = self.M
+        r = torch.linspace(self.r_lo, self.r_hi, M, dtype=torch.float64, device=dev)
+        eps = 1e-5 * (self.r_hi - self.r_lo)
+        pts = torch.cat([r, r + eps, r - eps]).contiguous()
+        samples = torch.empty(3 * M, D, dtype=torch.float64, device=dev)
+        K.mm_radial_mlp_f64(3 * M, pts, Ws[0], Ws[1], Ws[2], Ws[3], self.spec.num_bessel, Ws[1].shape[0], D,
+                            self.spec.r_max, self.spec.p_cutoff, mm.SILU_NORM, samples, stream())
+        coef = torch.empty(NCB * self.n_tab * (M - 1) * nW * 16 * 4, dtype=torch.float32, device=dev)
+        for tb in range(self.n_tab):
+            K.mm_spline_coeffs(samples, M, nW, eps, self.h, tb, self.n_tab, coef, stream())
+        return coef
+
+    # ------------------------------------------------------------------ workspace
+    def workspace(self, nC, n_nodes, E):
+        ws = self.ws
+        if ws is not None and ws["nC"] >= nC and ws["nN"] >= n_nodes and ws["E"] >= E:
+            return ws
+        nC = max(nC, ws["nC"] if ws else 0)
+        n_nodes = max(n_nodes, ws["nN"] if ws else 0)
+        E = max(E, ws["E"] if ws else 0)
+        self.ws = None
+        torch.cuda.empty_cache()
+        dev = self.dev
+        f = dict(dtype=torch.float32, device=dev)
+        i = dict(dtype=torch.int32, device=dev)
+        ws = dict(nC=nC, nN=n_nodes, E=E)
+        ws.update(e_vec=torch.empty(E, 3, **f), e_r=torch.empty(E, **f), e_Y=torch.empty(E, 16, **f),
+                  e_tab=torch.empty(E, **i), e_recv=torch.empty(E, **i), e_d=torch.empty(E, **f),
+                  e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
+        ws.update(spec=torch.empty(n_nodes, **i), lists=torch.empty(self.S * nC, **i), counts=torch.empty(self.S, **i))
+        ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
+                  rho=torch.empty(nC, **f), g_rho=torch.empty(nC, **f),
+                  M=torch.empty(nC * 16 * C, **f), gM=torch.empty(nC * 16 * C, **f),
+                  B=torch.empty(nC * 4 * C, **f), gB=torch.empty(nC * 4 * C, **f),
+                  h=torch.empty(nC * 4 * C, **f), gh=torch.empty(nC * 4 * C, **f),
+                  Xh=torch.empty(n_nodes * 4 * C, **f), gXh=torch.empty(n_nodes * 4 * C, **f))
+        self.ws = ws
+        return ws
+
+    # ------------------------------------------------------------------ helpers
+    def _lin(self, plan, inp, in_stride, out, out_stride, W, rows, in_rows=None, out_rows=None, scale=None,
+             scale_mode=0, species=False, accumulate=0, w_group_stride=0):
+        ws = self.ws
+        if species:
+            K.mm_linear(inp, in_stride, in_rows, out, out_stride, out_rows, W, scale, scale_mode, ws["lists"],
+                        ws["counts"], ws["nC"], self.S, w_group_stride, rows, accumulate, plan.n, plan.nsrc,
+                        plan.inoff, plan.widx, plan.outoff, stream())
+        else:
+            K.mm_linear(inp, in_stride, in_rows, out, out_stride, out_rows, W, scale, scale_mode, None, None, 0, 1, 0,
+                        rows, accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, stream())
+
+    def _geometry(self, k, g):
+        """Edge geometry of chunk g for interaction block k (LAMMPS pair vectors or positions)."""
+        ws = self.ws
+        sp = self.spec
+        if g.rij is not None:
+            K.mm_edge_geom_rij(g.nE, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
+                               sp.num_bessel, sp.r_max, sp.p_cutoff, ws["e_vec"], ws["e_r"], ws["e_Y"], ws["e_tab"],
+                               ws["e_recv"], ws["e_d"], ws["e_dd"], stream())
+        else:
+            K.mm_edge_geom_pos(g.nE, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
+                               self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, ws["e_vec"],
+                               ws["e_r"], ws["e_Y"], ws["e_tab"], ws["e_recv"], ws["e_d"], ws["e_dd"], stream())
+
+    def prepare(self, g):
+        """Per-chunk node species and per-species receiver lists (g.node_spec: compact species of local nodes)."""
+        ws = self.workspace(g.nC, g.n_nodes, g.nE)
+        ws["spec"][: g.n_nodes].copy_(g.node_spec)
+        K.mm_species_lists(ws["spec"], g.nC, self.S, ws["lists"], ws["nC"], ws["counts"], stream())
+        return ws
+
+    # ------------------------------------------------------------------ layer 1
+    def _layer1_forward(self, g, h1_out):
+        ws = self.ws
+        self._geometry(0, g)
+        K.mm_conv1_fwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], ws["e_d"], self.Xs1, ws["spec"], C,
+                       self.tab[0], self.n_tab, self.M, self.r_lo, self.inv_h, ws["A"], ws["rho"], stream())
+        self._lin(self.plan_l1, ws["A"], 16 * C, ws["M"], 16 * C, self.W_l1, g.nC, scale=ws["rho"], scale_mode=1,
+                  species=True, w_group_stride=4)
+        K.mm_symc1_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C, stream())
+        self._lin(self.plan_p1, ws["B"], 4 * C, h1_out, 4 * C, self.W_p1, g.nC)
+
+    def pass_a(self, g, H1):
+        """H1[a:b] = h1 of the chunk's receivers (pass A, mliap_threepass.py:504-519)."""
+        self.prepare(g)
+        self._layer1_forward(g, H1[g.a:g.b])
+
+    def pass_c(self, g, G1r, PF, eat):
+        """Layer 1 with gradient: eat[a:b] += scale R1(h1); PF[e0:e1] += d(scale R1 + G1r . h1)/dv
+        (mliap_threepass.py:564-582)."""
+        ws = self.prepare(g)
+        self._layer1_forward(g, ws["h"])
+        D1 = 4 * C
+        K.mm_readout1(g.nC, ws["h"], D1, self.r0s, self.scale, eat[g.a:g.b], G1r[g.a:g.b], D1, ws["gh"], D1, D1,
+                      stream())
+        self._lin(self.plan_p1, ws["gh"], D1, ws["gB"], D1, self.W_p1T, g.nC)
+        K.mm_symc1_bwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1, ws["gM"], 16 * C, ws["rho"],
+                       ws["g_rho"], stream())
+        self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=ws["rho"], scale_mode=1,
+                  species=True, w_group_stride=4)
+        K.mm_conv1_bwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], self.Xs1, ws["spec"], C, self.tab[0],
+                       self.n_tab, self.M, self.r_lo, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17, None, stream())
+        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
+                       PF[g.e0:g.e1], 1, stream())
+
+    # ------------------------------------------------------------------ layer 2
+    def pass_b(self, g, H1x, G1, PF, eat):
+        """Layer-2 energy with gradient: eat[a:b] += scale R2(h2); PF[e0:e1] = dE2/dv; G1[nodes] += dE2/dh1
+        (mliap_threepass.py:531-553)."""
+        ws = self.prepare(g)
+        D1 = 4 * C
+        h2, gh2, B2, gB2 = ws["h"], ws["gh"], ws["B"], ws["gB"]       # [nC, 128] views of the wider buffers
+        # sc = skip_tp(h1_recv) per species (0e part only), written into h2
+        self._lin(self.plan_sk1, H1x[g.a:g.b], D1, h2, C, self.W_sk1, g.nC, species=True, w_group_stride=1)
+        # node features of every local node: linear_up(H1x[nodes])
+        self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes)
+        self._geometry(1, g)
+        K.mm_conv2_fwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], ws["e_d"], ws["Xh"], None, D1,
+                       self.tab[1], self.n_tab, self.M, self.r_lo, self.inv_h, ws["A"], ws["rho"], stream())
+        self._lin(self.plan_lin2, ws["A"], self.nO2 * C, ws["M"], 16 * C, self.W_lin2, g.nC, scale=ws["rho"],
+                  scale_mode=1)
+        K.mm_symc2_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, B2, C, stream())
+        self._lin(self.plan_p2, B2, C, h2, C, self.W_p2, g.nC, accumulate=1)
+        K.mm_readout2(g.nC, h2, C, self.r1W1, self.r1w2, self.H_ro, mm.SILU_NORM, self.scale, eat[g.a:g.b], gh2, C,
+                      stream())
+        # ---- backward
+        self._lin(self.plan_p2, gh2, C, gB2, C, self.W_p2T, g.nC)
+        K.mm_symc2_bwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, gB2, C, ws["gM"], 16 * C, ws["rho"],
+                       ws["g_rho"], stream())
+        self._lin(self.plan_lin2T, ws["gM"], 16 * C, ws["gA"], self.nO2 * C, self.W_lin2T, g.nC, scale=ws["rho"],
+                  scale_mode=1)
+        K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
+        K.mm_conv2_bwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], ws["Xh"], None, D1, self.tab[1],
+                       self.n_tab, self.M, self.r_lo, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17, ws["gXh"],
+                       stream())
+        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
+                       PF[g.e0:g.e1], 0, stream())
+        self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)
+        self._lin(self.plan_sk1, gh2, C, G1[g.a:g.b], D1, self.W_sk1T, g.nC, species=True, w_group_stride=1,
+                  accumulate=1)

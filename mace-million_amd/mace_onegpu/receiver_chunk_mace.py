@@ -1,0 +1,221 @@
+"""Standalone receiver-chunked three-pass evaluator and its neighbour list (no LAMMPS).
+
+Mirrors mace_onegpu/receiver_chunk_mace.py of the reference:
+  * System (receiver_chunk_mace.py:91-165): positions wrapped and sorted in Morton order of cells, cell-list
+    neighbour list -- here built by the HIP kernels of csrc/nlist.hip (bit-exact with the reference), stored as a
+    CSR (rowptr int64 [N+1], senders int32 [E]) in the sorted index space;
+  * chunk topology (LocalGraph, receiver_chunk_mace.py:169-215, and ThreePassMLIAP._topology,
+    mliap_threepass.py:288-310): receivers of the chunk first, then the outside senders in ascending order;
+  * ReceiverChunkMACE.compute (receiver_chunk_mace.py:278-386): passes A, B, C over receiver chunks; edge vectors
+    are the fp64 minimum images of the sorted positions; forces F = -dE/dx in fp64.
+"""
+import ctypes
+import time
+
+import numpy as np
+import torch
+
+from ._lib import K, stream
+
+
+def host_f64(vals):
+    return ctypes.cast((ctypes.c_double * len(vals))(*[float(v) for v in vals]), ctypes.c_void_p)
+
+
+def host_i32(vals):
+    return ctypes.cast((ctypes.c_int * len(vals))(*[int(v) for v in vals]), ctypes.c_void_p)
+
+
+class System:
+    """Positions sorted in Morton order of cells; perm maps sorted -> original index.  pos [N, 3] fp64,
+    box [3], spidx [N] model element index; r_cut = cutoff of the neighbour list (r_max, or r_max + skin)."""
+
+    def __init__(self, pos, box, spidx, r_max, device="cuda"):
+        dev = torch.device(device)
+        self.device = dev
+        self.box = np.asarray(box, dtype=np.float64).reshape(3)
+        if not (self.box > 2 * r_max).all():
+            raise ValueError("minimum image needs box > 2 r_max in every direction")
+        self.r_max = float(r_max)
+        pos = torch.as_tensor(pos, dtype=torch.float64).to(dev).contiguous()
+        spidx = torch.as_tensor(spidx).to(dev).to(torch.int32).contiguous()
+        N = pos.shape[0]
+        self.N = N
+        self.ncell = np.maximum(np.floor(self.box / r_max).astype(np.int64), 1)
+        cs = self.box / self.ncell.astype(np.float64)
+        self._box_h, self._nc_h, self._cs_h = host_f64(self.box), host_i32(self.ncell), host_f64(cs)
+        pos_w = torch.empty_like(pos)
+        cell = torch.empty(N, 3, dtype=torch.int32, device=dev)
+        key = torch.empty(N, dtype=torch.int64, device=dev)
+        idx = torch.empty(N, dtype=torch.int64, device=dev)
+        K.mm_nl_prepare(pos, N, self._box_h, self._nc_h, self._cs_h, pos_w, cell, key, idx, stream())
+        nbytes = ctypes.c_size_t(0)
+        K.mm_nl_workspace_bytes(N + 1, ctypes.byref(nbytes))
+        self._ws = torch.empty(int(nbytes.value), dtype=torch.uint8, device=dev)
+        key_s = torch.empty_like(key)
+        perm = torch.empty_like(idx)
+        K.mm_nl_sort(key, key_s, idx, perm, N, self._ws, self._ws.numel(), stream())
+        self.perm = perm
+        self.pos = torch.empty_like(pos)
+        self.cell = torch.empty_like(cell)
+        self.spidx = torch.empty_like(spidx)
+        K.mm_nl_gather(perm, N, pos_w, cell, spidx, self.pos, self.cell, self.spidx, stream())
+        del pos_w, cell, key, idx, key_s
+
+    def min_image(self, v):
+        box = torch.as_tensor(self.box, dtype=v.dtype, device=v.device)
+        return v - box * torch.round(v / box)
+
+    def build_neighbors(self, r_cut=None):
+        """CSR neighbour list within r_cut (default r_max) in the reference's candidate order.  The cell grid
+        is the one of r_max (as System.__init__ fixes it), so r_cut must not exceed r_max unless the System was
+        created with r_max = r_cut."""
+        r_cut = self.r_max if r_cut is None else float(r_cut)
+        if r_cut > self.r_max:
+            raise ValueError("r_cut larger than the cell size of this System")
+        dev, N = self.device, self.N
+        nc = self.ncell
+        ncells = int(np.prod(nc))
+        brute = int((nc < 3).any())
+        start = torch.empty(ncells, dtype=torch.int32, device=dev)
+        count = torch.empty(ncells, dtype=torch.int32, device=dev)
+        K.mm_nl_cell_ranges(self.cell, N, self._nc_h, start, count, stream())
+        NN = torch.empty(N, dtype=torch.int32, device=dev)
+        r2 = r_cut ** 2
+        K.mm_nl_count(self.pos, self.cell, N, self._box_h, self._nc_h, start, count, r2, brute, NN, stream())
+        rowptr = torch.empty(N + 1, dtype=torch.int64, device=dev)
+        K.mm_nl_scan(NN, rowptr, N, self._ws, self._ws.numel(), stream())
+        E = int(rowptr[-1])
+        send = torch.empty(max(E, 1), dtype=torch.int32, device=dev)
+        K.mm_nl_fill(self.pos, self.cell, N, self._box_h, self._nc_h, start, count, r2, brute, rowptr, send,
+                     stream())
+        self.NN, self.rowptr, self.send = NN, rowptr, send[:E]
+        self.MN = int(NN.max()) if N else 0
+        return self.MN
+
+
+class ChunkGraph:
+    """Topology and inputs of one receiver chunk [a, b) whose edges are [e0, e1) of the receiver-sorted pairs."""
+    rij = None
+    pair_i = None
+    pos = None
+    box_host = None
+    recv_local = None
+
+
+def chunk_topology(a, b, e0, e1, pj, loc, flag):
+    """Receivers a..b-1 first, then the senders outside [a, b) in ascending order; int32 local sender index per
+    edge.  Restates ThreePassMLIAP._topology (mliap_threepass.py:288-310); loc (int32, -1) and flag (bool, False)
+    are scratch arrays over all atoms and are restored before returning."""
+    dev = pj.device
+    nC = b - a
+    send_g = pj[e0:e1].long()
+    loc[a:b] = torch.arange(nC, device=dev, dtype=loc.dtype)
+    flag[send_g] = True
+    flag[a:b] = False
+    new = torch.nonzero(flag).squeeze(1)
+    flag[new] = False
+    loc[new] = torch.arange(nC, nC + new.numel(), device=dev, dtype=loc.dtype)
+    nodes = torch.cat([torch.arange(a, b, device=dev, dtype=torch.int32), new.to(torch.int32)])
+    ls = loc[send_g].contiguous()
+    loc[nodes.long()] = -1
+    return nodes, ls
+
+
+def make_chunk(a, b, e0, e1, nodes, ls, rowptr_full, node_spec_all):
+    g = ChunkGraph()
+    g.a, g.b, g.e0, g.e1 = a, b, e0, e1
+    g.nC, g.nE = b - a, e1 - e0
+    g.nodes = nodes.contiguous()
+    g.n_nodes = nodes.numel()
+    g.ls = ls
+    g.rowptr = (rowptr_full[a:b + 1] - e0).to(torch.int32).contiguous()
+    g.node_spec = node_spec_all[g.nodes.long()].contiguous()
+    return g
+
+
+class ReceiverChunkMACE:
+    """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
+
+    def __init__(self, model, chunk=16384, spline_grid=512, device="cuda"):
+        self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
+        self.dev = torch.device(device)
+        self.fl = None
+        self.D1 = 4 * model.spec.C
+
+    def _layers(self, sysm):
+        from .fast_layers import FastLayers
+        cols = sorted(int(c) for c in torch.unique(sysm.spidx.long()).tolist())
+        if self.fl is None or self.fl.cols != cols:
+            self.fl = FastLayers(self.model, cols, self.spline_grid, device=self.dev)
+        return self.fl
+
+    def graphs(self, sysm):
+        """Topologies of all chunks (cached per neighbour list)."""
+        fl = self._layers(sysm)
+        dev, N = self.dev, sysm.N
+        rp = sysm.rowptr
+        rp_cpu = rp.cpu().numpy()
+        recv_all = torch.repeat_interleave(torch.arange(N, device=dev, dtype=torch.int32), sysm.NN.long())
+        loc = torch.full((N,), -1, dtype=torch.int32, device=dev)
+        flag = torch.zeros(N, dtype=torch.bool, device=dev)
+        node_spec_all = fl.col2s[sysm.spidx.long()]
+        box_h = host_f64(sysm.box)
+        out = []
+        for a in range(0, N, self.chunk):
+            b = min(a + self.chunk, N)
+            e0, e1 = int(rp_cpu[a]), int(rp_cpu[b])
+            nodes, ls = chunk_topology(a, b, e0, e1, sysm.send, loc, flag)
+            g = make_chunk(a, b, e0, e1, nodes, ls, rp, node_spec_all)
+            g.pos, g.box_host = sysm.pos, box_h
+            g.recv_local = (recv_all[e0:e1] - a).contiguous()
+            out.append(g)
+        return out
+
+    def compute(self, sysm, graphs=None, timings=None):
+        """Returns (E float, eat fp64 [N], F fp64 [N, 3], PF fp32 [E, 3]) in the sorted index space."""
+        fl = self._layers(sysm)
+        dev, N = self.dev, sysm.N
+        graphs = graphs if graphs is not None else self.graphs(sysm)
+        E = int(sysm.rowptr[-1])
+        t = {}
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        H1 = torch.zeros(N, self.D1, dtype=torch.float32, device=dev)
+        for g in graphs:
+            fl.pass_a(g, H1)
+        torch.cuda.synchronize()
+        t["A"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        G1 = torch.zeros_like(H1)
+        PF = torch.zeros(max(E, 1), 3, dtype=torch.float32, device=dev)
+        eat = torch.zeros(N, dtype=torch.float64, device=dev)
+        for g in graphs:
+            fl.pass_b(g, H1, G1, PF, eat)
+        torch.cuda.synchronize()
+        t["B"] = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        for g in graphs:
+            fl.pass_c(g, G1, PF, eat)
+        torch.cuda.synchronize()
+        t["C"] = time.perf_counter() - t0
+        eat += fl.e0[sysm.spidx.long()] + fl.shift
+        F = pair_to_atom_forces(sysm, PF)
+        if timings is not None:
+            timings.update(t)
+        self.H1, self.G1 = H1, G1
+        return float(eat.sum()), eat, F, PF[:E]
+
+
+def pair_to_atom_forces(sysm, PF):
+    """F_i = -sum_{e: recv=i} PF_e + sum_{e: send=i} PF_e (v_e = x_recv - x_send), deterministic CSR sums."""
+    dev, N = sysm.device, sysm.N
+    if not hasattr(sysm, "_s_perm") or sysm._s_perm_E != sysm.send.numel():
+        s_perm = torch.argsort(sysm.send.long(), stable=True)
+        cnt = torch.bincount(sysm.send.long(), minlength=N)
+        s_rowptr = torch.zeros(N + 1, dtype=torch.int64, device=dev)
+        s_rowptr[1:] = torch.cumsum(cnt, 0)
+        sysm._s_perm, sysm._s_rowptr, sysm._s_perm_E = s_perm, s_rowptr, sysm.send.numel()
+    F = torch.empty(N, 3, dtype=torch.float64, device=dev)
+    K.mm_pair_forces_to_atoms(N, sysm.rowptr, sysm._s_rowptr, sysm._s_perm, PF, F, stream())
+    return F
