@@ -1,0 +1,153 @@
+/* C ABI of libmace_million_amd.so: the MI355X (gfx950) kernels of the receiver-chunked three-pass MACE
+ * energy + force evaluation.
+ *
+ * Conventions (all entry points):
+ *   - return 0 on success, a negative code on failure (-1 invalid argument, -2 launch failure); the message of the
+ *     last failure of the calling thread is mm_last_error();
+ *   - pointers are device pointers unless marked HOST; sizes are element counts; `stream` is a hipStream_t;
+ *   - no entry point allocates, frees or synchronises: the caller owns every buffer, and every call can be
+ *     captured into a HIP graph;
+ *   - float features are stored "ir_mul": element (component j, channel c) of a node row at j * 128 + c.
+ * The reference reaches the same operations through Triton launches and cuEquivariance/torch calls; each
+ * declaration names the reference interface (file:line under the reference repository) that it replaces.
+ */
+#ifndef MACE_MILLION_AMD_H
+#define MACE_MILLION_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mm_stream_t; /* hipStream_t */
+
+/* ---------------------------------------------------------------------------------------------- library */
+const char* mm_last_error(void);
+int mm_version(void);
+/* channel count (128), channel blocks (8, one per XCD) and channels per block (16) the kernels were built for */
+int mm_build_info(int* channels, int* channel_blocks, int* block_channels);
+
+/* ---------------------------------------------------------------------------------------------- (1) neighbours
+ * Replace receiver_chunk_mace.System.__init__ / morton3 / build_neighbors (receiver_chunk_mace.py:82-165):
+ * wrap, Morton order, 27-cell candidate scan with fp64 minimum image; bit-exact edge sets and order. */
+int mm_nl_workspace_bytes(long N, size_t* bytes /* HOST */);
+int mm_nl_prepare(const double* pos_in, long N, const double* box /* HOST [3] */, const int* ncell /* HOST [3] */,
+                  const double* cell_size /* HOST [3] */, double* pos_wrapped, int* cell, long long* morton_key,
+                  long long* index, mm_stream_t stream);
+int mm_nl_sort(const long long* key_in, long long* key_out, const long long* index_in, long long* perm, long N,
+               void* workspace, size_t workspace_bytes, mm_stream_t stream);
+int mm_nl_gather(const long long* perm, long N, const double* pos_wrapped, const int* cell, const int* spec_in,
+                 double* pos_sorted, int* cell_sorted, int* spec_sorted, mm_stream_t stream);
+int mm_nl_cell_ranges(const int* cell_sorted, long N, const int* ncell /* HOST [3] */, int* cell_start,
+                      int* cell_count, mm_stream_t stream);
+int mm_nl_count(const double* pos_sorted, const int* cell_sorted, long N, const double* box /* HOST [3] */,
+                const int* ncell /* HOST [3] */, const int* cell_start, const int* cell_count, double r_cut2,
+                int brute, int* NN, mm_stream_t stream);
+int mm_nl_scan(const int* NN, long* rowptr, long N, void* workspace, size_t workspace_bytes, mm_stream_t stream);
+int mm_nl_fill(const double* pos_sorted, const int* cell_sorted, long N, const double* box /* HOST [3] */,
+               const int* ncell /* HOST [3] */, const int* cell_start, const int* cell_count, double r_cut2,
+               int brute, const long* rowptr, int* send, mm_stream_t stream);
+/* per-step pair list of an MD run: pairs of a skin list within r_max (LAMMPS' ML-IAP pair list within the
+ * cutoff, inputs/in.water_scan.lmp:44-52) */
+int mm_nl_filter_count(const double* pos, long N, const double* box /* HOST [3] */, const long* skin_rowptr,
+                       const int* skin_send, double r_max2, int* NN, mm_stream_t stream);
+int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] */, const long* skin_rowptr,
+                      const int* skin_send, double r_max2, const long* rowptr, int* send, mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- edge geometry
+ * Replace receiver_chunk_mace.edge_embed (:230-234) and the density part of FastLayers.layer1/layer2_energy
+ * (fast_layers.py:179-183, 190-192, 209-213): length, Y_lm l<=3, spline table index of the ordered species pair,
+ * local receiver, edge density tanh((B . w)^2) f_cut and its r-derivative.  dens_w is HOST [nb]. */
+int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* local_send,
+                     const int* node_spec, int S, const int* pair_map, const float* dens_w, int nb, float r_max,
+                     int p_cut, float* e_vec, float* e_r, float* e_Y, int* e_tab, int* e_recv, float* e_d,
+                     float* e_dd, mm_stream_t stream);
+int mm_edge_geom_pos(int E, const double* pos, const double* box /* HOST [3] */, const int* recv_local, int a,
+                     const int* local_send, const int* nodes, const int* node_spec, int S, const int* pair_map,
+                     const float* dens_w, int nb, float r_max, int p_cut, float* e_vec, float* e_r, float* e_Y,
+                     int* e_tab, int* e_recv, float* e_d, float* e_dd, mm_stream_t stream);
+/* per-edge dL/dv from the convolution backward partials, the density term and the SH chain rule (the autograd
+ * step torch.autograd.grad(..., [vec]) of mliap_threepass.py:550, 580) */
+int mm_edge_grad(int E, const float* part, long part_stride, int n_part, const float* g_rho, const int* e_recv,
+                 const float* e_dd, const float* e_vec, float* pair_force, int accumulate, mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- (2)+(3) edge conv
+ * Replace conv_spline.ConvSpline.forward / gen_fwd (conv_spline.py:38-94, 294-301), spline_w._w_fwd
+ * (spline_w.py:30-50) + FusedConvTP.forward (fused_conv.py:33-37): spline-table radial weights x channelwise TP x
+ * receiver-CSR sum; and their backward (conv_spline.gen_bwd :97-181, spline_w._w_bwd :53-75): per-edge
+ * dL/dr, dL/dY partials per channel block, optional dL/dX (layer 2, G1 path).  tab: interval coefficients built by
+ * mm_spline_coeffs.  Layer 1: nX=1, nW=4, nO=16; layer 2: nX=4, nW=10, nO=40. */
+int mm_conv1_fwd(const int* rowptr, int nC, const float* e_r, const int* e_tab, const int* e_send,
+                 const float* e_Y, const float* e_d, const float* X, const int* xrow, int x_stride,
+                 const float* tab, int n_tab, int M, float r_lo, float inv_h, float* out, float* rho,
+                 mm_stream_t stream);
+int mm_conv2_fwd(const int* rowptr, int nC, const float* e_r, const int* e_tab, const int* e_send,
+                 const float* e_Y, const float* e_d, const float* X, const int* xrow, int x_stride,
+                 const float* tab, int n_tab, int M, float r_lo, float inv_h, float* out, float* rho,
+                 mm_stream_t stream);
+int mm_conv1_bwd(const int* rowptr, int nC, const float* e_r, const int* e_tab, const int* e_send,
+                 const float* e_Y, const float* X, const int* xrow, int x_stride, const float* tab, int n_tab, int M,
+                 float r_lo, float inv_h, const float* gA, float* part, long part_stride, float* gX,
+                 mm_stream_t stream);
+int mm_conv2_bwd(const int* rowptr, int nC, const float* e_r, const int* e_tab, const int* e_send,
+                 const float* e_Y, const float* X, const int* xrow, int x_stride, const float* tab, int n_tab, int M,
+                 float r_lo, float inv_h, const float* gA, float* part, long part_stride, float* gX,
+                 mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- (4) node level
+ * Symmetric contraction (correlation 3, per species) forward / backward: replaces model.products[k]
+ * .symmetric_contractions (graphed_three_pass.py:56-57; cuEquivariance kernel in the reference). */
+int mm_symc1_fwd(int n, const float* x, long x_stride, const int* spec, const float* Wsc, float* out,
+                 long out_stride, mm_stream_t stream);
+int mm_symc2_fwd(int n, const float* x, long x_stride, const int* spec, const float* Wsc, float* out,
+                 long out_stride, mm_stream_t stream);
+int mm_symc1_bwd(int n, const float* x, long x_stride, const int* spec, const float* Wsc, const float* gout,
+                 long gout_stride, float* gx, long gx_stride, const float* rho, float* g_rho, mm_stream_t stream);
+int mm_symc2_bwd(int n, const float* x, long x_stride, const int* spec, const float* Wsc, const float* gout,
+                 long gout_stride, float* gx, long gx_stride, const float* rho, float* g_rho, mm_stream_t stream);
+/* Equivariant linears on MFMA: linear_up, linear (with / (rho+1)), species-block skip_tp (replaces
+ * fast_layers.SpeciesSkip, fast_layers.py:41-105), product linear, and transposes.  comp_* are HOST arrays:
+ * nsrc [n_comp], in_off / w_idx [n_comp][3], out_off [n_comp]. */
+int mm_linear(const float* in, long in_stride, const int* in_rows, float* out, long out_stride, const int* out_rows,
+              const float* W, const float* row_scale, int scale_mode, const int* list, const int* list_count,
+              long list_stride, int n_groups, int w_group_stride, int n_rows_max, int accumulate, int n_comp,
+              const int* comp_nsrc, const int* comp_in_off, const int* comp_w_idx, const int* comp_out_off,
+              mm_stream_t stream);
+int mm_species_lists(const int* spec, int n, int S, int* lists, long stride, int* counts, mm_stream_t stream);
+/* readouts with energy accumulation and gradient: model.readouts[0] / [1] and the losses of passes B and C
+ * (mliap_threepass.py:550, 578-579) */
+int mm_readout1(int n, const float* h1, long h_stride, const float* w0, float scale, double* eat, const float* g1r,
+                long g1_stride, float* gh, long gh_stride, int D, mm_stream_t stream);
+int mm_readout2(int n, const float* h2, long h_stride, const float* W1, const float* w2, int H, float cst,
+                float scale, double* eat, float* gh, long gh_stride, mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- (5) exchange
+ * Ghost exchange on one GPU (periodic images): data.forward_exchange / data.reverse_exchange
+ * (mliap_threepass.py:40-55, 522, 556). */
+int mm_ghost_forward(const float* src, float* dst, int D, int nlocal, int nghost, const int* owner,
+                     mm_stream_t stream);
+int mm_ghost_reverse(const float* src, float* dst, int D, int nlocal, const int* ghost_rowptr, const int* ghost_list,
+                     mm_stream_t stream);
+/* per-atom forces from pair forces (ReceiverChunkMACE._accum_forces, receiver_chunk_mace.py:272-276) */
+int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* send_rowptr, const long* send_perm,
+                            const float* pair_force, double* F, mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- tables
+ * conv_spline.build_tables + spline_radial._sample (conv_spline.py:230-249, spline_radial.py:116-151): the radial
+ * MLP x cutoff in fp64 at grid points, then the cubic interval coefficients. */
+int mm_radial_mlp_f64(int n_pts, const double* r_pts, const double* W0, const double* W1, const double* W2,
+                      const double* W3, int nb, int H, int D, double r_max, int p_cut, double silu_cst, double* out,
+                      mm_stream_t stream);
+int mm_spline_coeffs(const double* samples, int M, int nW, double eps, double h, int tab, int n_tab, float* coef,
+                     mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- utilities */
+int mm_fill_f32(float* p, long n, float v, mm_stream_t stream);
+int mm_fill_f64(double* p, long n, double v, mm_stream_t stream);
+int mm_fill_i32(int* p, long n, int v, mm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MACE_MILLION_AMD_H */

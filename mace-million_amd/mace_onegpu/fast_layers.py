@@ -154,6 +154,32 @@ class FastLayers:
                                    for w in range(len(mid_ls)) for m in range(2 * mid_ls[w] + 1)])
         self.nO1, self.nO2 = self.tables.tp1["nO"], self.tables.tp2["nO"]
         self.ws = None
+        self.ktimer = None        # list of (name, units, start event, end event) while kernel timing is on
+
+    # ------------------------------------------------------------------ per-launch timing (HIP events)
+    def start_kernel_timing(self):
+        self.ktimer = []
+
+    def stop_kernel_timing(self):
+        """{name: dict(launches, ms_total, units)} of the timed launches; synchronises."""
+        torch.cuda.synchronize()
+        out = {}
+        for name, units, e0, e1 in self.ktimer or []:
+            d = out.setdefault(name, dict(launches=0, ms_total=0.0, units=[]))
+            d["launches"] += 1
+            d["ms_total"] += e0.elapsed_time(e1)
+            d["units"].append(units)
+        self.ktimer = None
+        return out
+
+    def _timed(self, name, units, fn, *args):
+        if self.ktimer is None:
+            return fn(*args)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn(*args)
+        e1.record()
+        self.ktimer.append((name, units, e0, e1))
 
     # ------------------------------------------------------------------ tables
     def _build_table(self, P, k):
@@ -237,8 +263,9 @@ class FastLayers:
     def _layer1_forward(self, g, h1_out):
         ws = self.ws
         self._geometry(0, g)
-        K.mm_conv1_fwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], ws["e_d"], self.Xs1, ws["spec"], C,
-                       self.tab[0], self.n_tab, self.M, self.r_lo, self.inv_h, ws["A"], ws["rho"], stream())
+        self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
+                    g.ls, ws["e_Y"], ws["e_d"], self.Xs1, ws["spec"], C, self.tab[0], self.n_tab, self.M, self.r_lo,
+                    self.inv_h, ws["A"], ws["rho"], stream())
         self._lin(self.plan_l1, ws["A"], 16 * C, ws["M"], 16 * C, self.W_l1, g.nC, scale=ws["rho"], scale_mode=1,
                   species=True, w_group_stride=4)
         K.mm_symc1_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C, stream())
@@ -262,8 +289,9 @@ class FastLayers:
                        ws["g_rho"], stream())
         self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=ws["rho"], scale_mode=1,
                   species=True, w_group_stride=4)
-        K.mm_conv1_bwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], self.Xs1, ws["spec"], C, self.tab[0],
-                       self.n_tab, self.M, self.r_lo, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17, None, stream())
+        self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
+                    g.ls, ws["e_Y"], self.Xs1, ws["spec"], C, self.tab[0], self.n_tab, self.M, self.r_lo, self.inv_h,
+                    ws["gA"], ws["part"], ws["E"] * 17, None, stream())
         K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
                        PF[g.e0:g.e1], 1, stream())
 
@@ -279,8 +307,9 @@ class FastLayers:
         # node features of every local node: linear_up(H1x[nodes])
         self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes)
         self._geometry(1, g)
-        K.mm_conv2_fwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], ws["e_d"], ws["Xh"], None, D1,
-                       self.tab[1], self.n_tab, self.M, self.r_lo, self.inv_h, ws["A"], ws["rho"], stream())
+        self._timed("conv2_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_fwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
+                    g.ls, ws["e_Y"], ws["e_d"], ws["Xh"], None, D1, self.tab[1], self.n_tab, self.M, self.r_lo,
+                    self.inv_h, ws["A"], ws["rho"], stream())
         self._lin(self.plan_lin2, ws["A"], self.nO2 * C, ws["M"], 16 * C, self.W_lin2, g.nC, scale=ws["rho"],
                   scale_mode=1)
         K.mm_symc2_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, B2, C, stream())
@@ -294,9 +323,9 @@ class FastLayers:
         self._lin(self.plan_lin2T, ws["gM"], 16 * C, ws["gA"], self.nO2 * C, self.W_lin2T, g.nC, scale=ws["rho"],
                   scale_mode=1)
         K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
-        K.mm_conv2_bwd(g.rowptr, g.nC, ws["e_r"], ws["e_tab"], g.ls, ws["e_Y"], ws["Xh"], None, D1, self.tab[1],
-                       self.n_tab, self.M, self.r_lo, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17, ws["gXh"],
-                       stream())
+        self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
+                    g.ls, ws["e_Y"], ws["Xh"], None, D1, self.tab[1], self.n_tab, self.M, self.r_lo, self.inv_h,
+                    ws["gA"], ws["part"], ws["E"] * 17, ws["gXh"], stream())
         K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
                        PF[g.e0:g.e1], 0, stream())
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)

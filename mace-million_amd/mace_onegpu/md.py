@@ -1,0 +1,119 @@
+"""Velocity-Verlet molecular dynamics driven by the three-pass evaluator (benchmark configuration 5).
+
+The reference runs MD through LAMMPS (inputs/in.water_scan.lmp: nve, neighbour skin, ML-IAP pair list within the
+cutoff every step) and benchmarks the evaluator standalone (graphed_three_pass.py).  This driver keeps the whole
+step on the GPU:
+  * a skin neighbour list (cell list with r_cut = r_max + skin, System: Morton-sorted atoms, bit-exact build);
+  * every step the pairs within r_max are filtered from the skin list (mm_nl_filter_*, candidate order kept);
+  * energy + forces by ReceiverChunkMACE (three passes over receiver chunks);
+  * kick-drift-kick velocity Verlet in metal units (eV, A, ps, amu; 1 eV/(A amu) = 9648.533 A/ps^2);
+  * the skin list is rebuilt (atoms re-sorted, velocities and masses permuted with them) as soon as an atom has
+    moved more than skin / 2 since the last build.
+"""
+import numpy as np
+import torch
+
+from ._lib import K, stream
+from .receiver_chunk_mace import ReceiverChunkMACE, System, host_f64
+from .systems import maxwell_boltzmann
+
+ACC = 9648.533212331          # eV / (A amu) -> A / ps^2
+
+
+class PairList:
+    """Pairs within r_max filtered from a skin list (same fields as System for ReceiverChunkMACE)."""
+
+    def __init__(self, skin_sys, r_max):
+        self.N, self.device, self.box = skin_sys.N, skin_sys.device, skin_sys.box
+        self.pos, self.spidx = skin_sys.pos, skin_sys.spidx
+        self.r_max = r_max
+        self._skin = skin_sys
+        self._box_h = host_f64(skin_sys.box)
+        self.NN = torch.empty(self.N, dtype=torch.int32, device=self.device)
+        self.rowptr = torch.empty(self.N + 1, dtype=torch.int64, device=self.device)
+        self.send = None
+
+    def refresh(self):
+        s = self._skin
+        r2 = self.r_max ** 2
+        K.mm_nl_filter_count(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.NN, stream())
+        K.mm_nl_scan(self.NN, self.rowptr, self.N, s._ws, s._ws.numel(), stream())
+        E = int(self.rowptr[-1])
+        if self.send is None or self.send.numel() < E:
+            self.send = torch.empty(int(E * 1.1) + 1, dtype=torch.int32, device=self.device)
+        K.mm_nl_filter_fill(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.rowptr, self.send, stream())
+        self.E = E
+        self.send_view = self.send[:E]
+        return E
+
+
+class MDRunner:
+    def __init__(self, model, pos, box, Z, chunk=65536, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device="cuda",
+                 spline_grid=512):
+        self.model = model
+        self.dev = torch.device(device)
+        self.r_max = float(model.spec.r_max)
+        self.skin = float(skin)
+        self.dt = dt_fs * 1e-3                          # ps
+        self.box = np.asarray(box, dtype=np.float64)
+        Z = np.asarray(Z)
+        v, m = maxwell_boltzmann(Z, T, seed_v)
+        self.Z = torch.as_tensor(Z, device=self.dev)
+        self.vel = torch.as_tensor(v, dtype=torch.float64, device=self.dev)
+        self.mass = torch.as_tensor(m, dtype=torch.float64, device=self.dev)
+        self.gid = torch.arange(len(Z), device=self.dev)       # original atom index of each current slot
+        self.ev = ReceiverChunkMACE(model, chunk=chunk, spline_grid=spline_grid, device=self.dev)
+        self.n_rebuild = 0
+        self._build(torch.as_tensor(pos, dtype=torch.float64, device=self.dev))
+        self.F = None
+        self.E = None
+
+    def _build(self, pos):
+        spidx = (self.Z - 1).to(torch.int32)
+        s = System(pos, self.box, spidx, self.r_max + self.skin, device=self.dev)
+        perm = s.perm
+        self.vel, self.mass, self.Z, self.gid = self.vel[perm], self.mass[perm], self.Z[perm], self.gid[perm]
+        s.build_neighbors()
+        self.skin_sys = s
+        self.pos = s.pos                                   # updated in place by the integrator
+        self.x_build = s.pos.clone()
+        self.pairs = PairList(s, self.r_max)
+        self.n_rebuild += 1
+
+    def forces(self):
+        pl = self.pairs
+        pl.refresh()
+        view = _PairView(pl)
+        E, eat, F, PF = self.ev.compute(view)
+        self.E, self.F = E, F
+        return E, F
+
+    def _maybe_rebuild(self):
+        disp = (self.pos - self.x_build).norm(dim=1).max()
+        if float(disp) > 0.5 * self.skin:
+            self._build(self.pos.clone())
+            return True
+        return False
+
+    def step(self):
+        if self.F is None:
+            self.forces()
+        a = self.F / self.mass[:, None] * ACC
+        self.vel.add_(0.5 * self.dt * a)
+        self.pos.add_(self.dt * self.vel)
+        rebuilt = self._maybe_rebuild()
+        self.forces()
+        a = self.F / self.mass[:, None] * ACC
+        self.vel.add_(0.5 * self.dt * a)
+        return rebuilt
+
+    def kinetic(self):
+        return float(0.5 * (self.mass[:, None] * self.vel ** 2).sum() / ACC)
+
+
+class _PairView:
+    """System-like view of a PairList for ReceiverChunkMACE (send trimmed to the current pair count)."""
+
+    def __init__(self, pl):
+        self.N, self.device, self.box, self.pos, self.spidx = pl.N, pl.device, pl.box, pl.pos, pl.spidx
+        self.NN, self.rowptr, self.send = pl.NN, pl.rowptr, pl.send_view

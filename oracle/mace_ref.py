@@ -30,9 +30,12 @@ SILU_NORM_QUAD = None     # computed lazily by quadrature (independent of the pr
 def silu_norm():
     global SILU_NORM_QUAD
     if SILU_NORM_QUAD is None:
+        import warnings
         from scipy.integrate import quad
-        v, _ = quad(lambda z: (z / (1 + math.exp(-z))) ** 2 * math.exp(-z * z / 2) / math.sqrt(2 * math.pi),
-                    -40, 40, epsabs=1e-15, epsrel=1e-14, limit=500)
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")
+            v, _ = quad(lambda z: (z / (1 + math.exp(-z))) ** 2 * math.exp(-z * z / 2) / math.sqrt(2 * math.pi),
+                        -40, 40, epsabs=1e-15, epsrel=1e-14, limit=500)
         SILU_NORM_QUAD = 1.0 / math.sqrt(v)
     return SILU_NORM_QUAD
 
@@ -311,7 +314,7 @@ def energy_forces_full(m, pos, box, spec, recv, send, tables=None):
     e = energy_full(m, pos, box, spec, recv, send, tables)
     E = e.sum()
     (g,) = torch.autograd.grad(E, [pos])
-    return float(E), e.detach(), (-g).detach()
+    return float(E.detach()), e.detach(), (-g).detach()
 
 
 # ----------------------------------------------------------------------------- three-pass (ReceiverChunkMACE)
