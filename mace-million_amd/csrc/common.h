@@ -42,3 +42,18 @@ __device__ __forceinline__ int mm_xcd_channel_block() {
   // channel block whose table slice that XCD keeps in its L2
   return blockIdx.x & (MM_NCB - 1);
 }
+
+// DPP (data-parallel primitive) lane moves inside a row of 16 lanes; used for channel reductions without LDS.
+template <int CTRL>
+__device__ __forceinline__ float mm_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the (bitwise identical) sum.
+__device__ __forceinline__ float mm_row_sum16(float v) {
+  v += mm_dpp<0xB1>(v);    // quad_perm [1, 0, 3, 2]: pairs within a quad
+  v += mm_dpp<0x4E>(v);    // quad_perm [2, 3, 0, 1]: quad sums
+  v += mm_dpp<0x141>(v);   // row_half_mirror: lane i <- 7 - i within each 8-lane half: 8-lane sums
+  v += mm_dpp<0x140>(v);   // row_mirror: lane i <- 15 - i: 16-lane sums
+  return v;
+}

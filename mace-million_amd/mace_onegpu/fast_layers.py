@@ -200,6 +200,11 @@ class FastLayers:
             K.mm_spline_coeffs(samples, M, nW, eps, self.h, tb, self.n_tab, coef, stream())
         return coef
 
+    def layer1_cache(self, n_atoms):
+        """Pass-A cache of the layer-1 message and density for n_atoms receivers (8 KiB per atom)."""
+        return dict(M=torch.empty(n_atoms, 16 * C, dtype=torch.float32, device=self.dev),
+                    rho=torch.empty(n_atoms, dtype=torch.float32, device=self.dev))
+
     # ------------------------------------------------------------------ workspace
     def workspace(self, nC, n_nodes, E):
         ws = self.ws
@@ -214,9 +219,8 @@ class FastLayers:
         f = dict(dtype=torch.float32, device=dev)
         i = dict(dtype=torch.int32, device=dev)
         ws = dict(nC=nC, nN=n_nodes, E=E)
-        ws.update(e_vec=torch.empty(E, 3, **f), e_r=torch.empty(E, **f), e_Y=torch.empty(E, 16, **f),
-                  e_tab=torch.empty(E, **i), e_recv=torch.empty(E, **i), e_d=torch.empty(E, **f),
-                  e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
+        ws.update(e_vec=torch.empty(E, 3, **f), e_Y=torch.empty(E, 16, **f), e_pk=torch.empty(E, 4, **f),
+                  e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
         ws.update(spec=torch.empty(n_nodes, **i), lists=torch.empty(self.S * nC, **i), counts=torch.empty(self.S, **i))
         ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
                   rho=torch.empty(nC, **f), g_rho=torch.empty(nC, **f),
@@ -243,14 +247,16 @@ class FastLayers:
         """Edge geometry of chunk g for interaction block k (LAMMPS pair vectors or positions)."""
         ws = self.ws
         sp = self.spec
+        x_from_spec = 1 if k == 0 else 0          # layer-1 sender features depend on the species only
         if g.rij is not None:
             K.mm_edge_geom_rij(g.nE, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
-                               sp.num_bessel, sp.r_max, sp.p_cutoff, ws["e_vec"], ws["e_r"], ws["e_Y"], ws["e_tab"],
-                               ws["e_recv"], ws["e_d"], ws["e_dd"], stream())
+                               sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo, self.inv_h, x_from_spec,
+                               ws["e_vec"], ws["e_Y"], ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
         else:
             K.mm_edge_geom_pos(g.nE, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
-                               self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, ws["e_vec"],
-                               ws["e_r"], ws["e_Y"], ws["e_tab"], ws["e_recv"], ws["e_d"], ws["e_dd"], stream())
+                               self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo,
+                               self.inv_h, x_from_spec, ws["e_vec"], ws["e_Y"], ws["e_pk"], ws["e_recv"],
+                               ws["e_dd"], stream())
 
     def prepare(self, g):
         """Per-chunk node species and per-species receiver lists (g.node_spec: compact species of local nodes)."""
@@ -260,38 +266,49 @@ class FastLayers:
         return ws
 
     # ------------------------------------------------------------------ layer 1
-    def _layer1_forward(self, g, h1_out):
+    def _layer1_forward(self, g, h1_out, M_out, rho_out):
+        """h1 of the chunk's receivers; M_out / rho_out receive the density-normalised message (symmetric
+        contraction input) and the density."""
         ws = self.ws
         self._geometry(0, g)
-        self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
-                    g.ls, ws["e_Y"], ws["e_d"], self.Xs1, ws["spec"], C, self.tab[0], self.n_tab, self.M, self.r_lo,
-                    self.inv_h, ws["A"], ws["rho"], stream())
-        self._lin(self.plan_l1, ws["A"], 16 * C, ws["M"], 16 * C, self.W_l1, g.nC, scale=ws["rho"], scale_mode=1,
+        self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+                    self.Xs1, C, self.tab[0], self.n_tab, self.M, ws["A"], rho_out, stream())
+        self._lin(self.plan_l1, ws["A"], 16 * C, M_out, 16 * C, self.W_l1, g.nC, scale=rho_out, scale_mode=1,
                   species=True, w_group_stride=4)
-        K.mm_symc1_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C, stream())
+        K.mm_symc1_fwd(g.nC, M_out, 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C, stream())
         self._lin(self.plan_p1, ws["B"], 4 * C, h1_out, 4 * C, self.W_p1, g.nC)
 
-    def pass_a(self, g, H1):
-        """H1[a:b] = h1 of the chunk's receivers (pass A, mliap_threepass.py:504-519)."""
-        self.prepare(g)
-        self._layer1_forward(g, H1[g.a:g.b])
-
-    def pass_c(self, g, G1r, PF, eat):
-        """Layer 1 with gradient: eat[a:b] += scale R1(h1); PF[e0:e1] += d(scale R1 + G1r . h1)/dv
-        (mliap_threepass.py:564-582)."""
+    def pass_a(self, g, H1, cache=None):
+        """H1[a:b] = h1 of the chunk's receivers (pass A, mliap_threepass.py:504-519).  With cache (dict of
+        M [N, 16*128] and rho [N]) the layer-1 message and density of the chunk are kept for pass C."""
         ws = self.prepare(g)
-        self._layer1_forward(g, ws["h"])
+        if cache is None:
+            self._layer1_forward(g, H1[g.a:g.b], ws["M"], ws["rho"])
+        else:
+            self._layer1_forward(g, H1[g.a:g.b], cache["M"][g.a:g.b], cache["rho"][g.a:g.b])
+
+    def pass_c(self, g, G1r, PF, eat, H1=None, cache=None):
+        """Layer 1 with gradient: eat[a:b] += scale R1(h1); PF[e0:e1] += d(scale R1 + G1r . h1)/dv
+        (mliap_threepass.py:564-582).  With the pass-A cache (and H1), the layer-1 forward is not recomputed: the
+        stored message, density and h1 are exactly what the recomputation would produce."""
+        ws = self.prepare(g)
+        if cache is None:
+            h1, Mc, rho = ws["h"], ws["M"], ws["rho"]
+            self._layer1_forward(g, h1, Mc, rho)
+        else:
+            h1, Mc, rho = H1[g.a:g.b], cache["M"][g.a:g.b], cache["rho"][g.a:g.b]
+            self._geometry(0, g)
         D1 = 4 * C
-        K.mm_readout1(g.nC, ws["h"], D1, self.r0s, self.scale, eat[g.a:g.b], G1r[g.a:g.b], D1, ws["gh"], D1, D1,
+        K.mm_readout1(g.nC, h1, D1, self.r0s, self.scale, eat[g.a:g.b], G1r[g.a:g.b], D1, ws["gh"], D1, D1,
                       stream())
         self._lin(self.plan_p1, ws["gh"], D1, ws["gB"], D1, self.W_p1T, g.nC)
-        K.mm_symc1_bwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1, ws["gM"], 16 * C, ws["rho"],
-                       ws["g_rho"], stream())
-        self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=ws["rho"], scale_mode=1,
+        K.mm_symc1_bwd(g.nC, Mc, 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1, ws["gM"], 16 * C, rho, ws["g_rho"],
+                       stream())
+        self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=rho, scale_mode=1,
                   species=True, w_group_stride=4)
-        self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
-                    g.ls, ws["e_Y"], self.Xs1, ws["spec"], C, self.tab[0], self.n_tab, self.M, self.r_lo, self.inv_h,
-                    ws["gA"], ws["part"], ws["E"] * 17, None, stream())
+        self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+                    self.Xs1, C, self.tab[0], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17,
+                    None, stream())
         K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
                        PF[g.e0:g.e1], 1, stream())
 
@@ -307,9 +324,8 @@ class FastLayers:
         # node features of every local node: linear_up(H1x[nodes])
         self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes)
         self._geometry(1, g)
-        self._timed("conv2_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_fwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
-                    g.ls, ws["e_Y"], ws["e_d"], ws["Xh"], None, D1, self.tab[1], self.n_tab, self.M, self.r_lo,
-                    self.inv_h, ws["A"], ws["rho"], stream())
+        self._timed("conv2_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+                    ws["Xh"], D1, self.tab[1], self.n_tab, self.M, ws["A"], ws["rho"], stream())
         self._lin(self.plan_lin2, ws["A"], self.nO2 * C, ws["M"], 16 * C, self.W_lin2, g.nC, scale=ws["rho"],
                   scale_mode=1)
         K.mm_symc2_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, B2, C, stream())
@@ -323,9 +339,9 @@ class FastLayers:
         self._lin(self.plan_lin2T, ws["gM"], 16 * C, ws["gA"], self.nO2 * C, self.W_lin2T, g.nC, scale=ws["rho"],
                   scale_mode=1)
         K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
-        self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_r"], ws["e_tab"],
-                    g.ls, ws["e_Y"], ws["Xh"], None, D1, self.tab[1], self.n_tab, self.M, self.r_lo, self.inv_h,
-                    ws["gA"], ws["part"], ws["E"] * 17, ws["gXh"], stream())
+        self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+                    ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17,
+                    ws["gXh"], stream())
         K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
                        PF[g.e0:g.e1], 0, stream())
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)

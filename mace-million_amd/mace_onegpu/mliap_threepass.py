@@ -35,7 +35,7 @@ CHEMICAL_SYMBOLS = [
     "Ir", "Pt", "Au", "Hg", "Tl", "Pb", "Bi", "Po", "At", "Rn", "Fr", "Ra", "Ac"]
 
 _RUNTIME = ("_fl", "_dev", "_cols", "_e0", "_loc", "_flag", "_log", "_D1", "_gx", "_use_graphs", "_fmax_abort",
-            "_t_end", "_peak", "_topo")
+            "_t_end", "_peak", "_topo", "_cache_l1", "_l1cache")
 
 _INT_MAX = 2 ** 31 - 1
 
@@ -100,6 +100,10 @@ class ThreePassMLIAP(MLIAPUnified):
         self._flag = None
         self._D1 = 4 * self.model.spec.C
         self._fmax_abort = float(os.environ.get("MACE3P_FMAX_ABORT", "100.0"))
+        # MACE3P_CACHE_L1=1 (default): pass A keeps the layer-1 message and density of every local atom
+        # (8 KiB per atom) and pass C reuses them instead of recomputing layer 1
+        self._cache_l1 = os.environ.get("MACE3P_CACHE_L1", "1") == "1"
+        self._l1cache = None
         self._use_graphs = os.environ.get("MACE3P_GRAPHS", "0") == "1"
         self._gx = None
         self._peak = 0.0
@@ -168,8 +172,13 @@ class ThreePassMLIAP(MLIAPUnified):
         # ---------------- pass A
         t0 = time.perf_counter()
         H1 = torch.zeros(nt, D1, dtype=torch.float32, device=dev)
+        cache = None
+        if self._cache_l1:
+            if self._l1cache is None or self._l1cache["rho"].numel() < nl:
+                self._l1cache = fl.layer1_cache(nl)
+            cache = self._l1cache
         for g in graphs:
-            fl.pass_a(g, H1)
+            fl.pass_a(g, H1, cache)
         H1x = torch.empty_like(H1)
         _exchange(data.forward_exchange, H1, H1x, D1)
         del H1
@@ -180,7 +189,8 @@ class ThreePassMLIAP(MLIAPUnified):
         G1 = torch.zeros_like(H1x)
         for g in graphs:
             fl.pass_b(g, H1x, G1, PF, eat)
-        del H1x
+        if cache is None:
+            del H1x
         G1r = torch.empty_like(G1)
         _exchange(data.reverse_exchange, G1, G1r, D1)
         del G1
@@ -189,7 +199,10 @@ class ThreePassMLIAP(MLIAPUnified):
         # ---------------- pass C
         t0 = time.perf_counter()
         for g in graphs:
-            fl.pass_c(g, G1r, PF, eat)
+            if cache is None:
+                fl.pass_c(g, G1r, PF, eat)
+            else:
+                fl.pass_c(g, G1r, PF, eat, H1x, cache)
         del G1r
         torch.cuda.synchronize()
         t["C"] = time.perf_counter() - t0

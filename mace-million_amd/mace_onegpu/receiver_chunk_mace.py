@@ -137,11 +137,14 @@ def make_chunk(a, b, e0, e1, nodes, ls, rowptr_full, node_spec_all):
 class ReceiverChunkMACE:
     """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
 
-    def __init__(self, model, chunk=16384, spline_grid=512, device="cuda"):
+    def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True):
         self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
         self.dev = torch.device(device)
         self.fl = None
         self.D1 = 4 * model.spec.C
+        # keep pass A's layer-1 message and density (8 KiB per atom) so that pass C does not recompute them
+        self.cache_layer1 = bool(cache_layer1)
+        self._cache = None
 
     def _layers(self, sysm):
         from .fast_layers import FastLayers
@@ -182,8 +185,13 @@ class ReceiverChunkMACE:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         H1 = torch.zeros(N, self.D1, dtype=torch.float32, device=dev)
+        cache = None
+        if self.cache_layer1:
+            if self._cache is None or self._cache["rho"].numel() < N:
+                self._cache = fl.layer1_cache(N)
+            cache = self._cache
         for g in graphs:
-            fl.pass_a(g, H1)
+            fl.pass_a(g, H1, cache)
         torch.cuda.synchronize()
         t["A"] = time.perf_counter() - t0
         t0 = time.perf_counter()
@@ -196,7 +204,7 @@ class ReceiverChunkMACE:
         t["B"] = time.perf_counter() - t0
         t0 = time.perf_counter()
         for g in graphs:
-            fl.pass_c(g, G1, PF, eat)
+            fl.pass_c(g, G1, PF, eat, H1, cache)
         torch.cuda.synchronize()
         t["C"] = time.perf_counter() - t0
         eat += fl.e0[sysm.spidx.long()] + fl.shift

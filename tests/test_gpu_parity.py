@@ -251,3 +251,15 @@ def test_md_steps_conserve_energy(dev, model):
     drift = max(e_tot) - min(e_tot)
     _say(f"  MD: E_tot range {drift:.3e} eV over 10 steps, KE {md.kinetic():.3f} eV")
     assert drift < 1e-3 * md.kinetic()
+
+
+def test_layer1_cache_matches_recompute(dev, model, water_gpu):
+    """Pass C reusing pass A's layer-1 message/density gives the recomputed result.  (Not bitwise: pass B's
+    sender-feature gradient is scattered with fp32 atomics, so G1 differs between any two runs at the rounding
+    level, as the reference's index_add_ / tl.atomic_add do.)"""
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
+    s = water_gpu
+    a = ReceiverChunkMACE(model, chunk=64, device=dev, cache_layer1=True).compute(s)
+    b = ReceiverChunkMACE(model, chunk=64, device=dev, cache_layer1=False).compute(s)
+    assert abs(a[0] - b[0]) < 1e-9 * s.N
+    assert float((a[3] - b[3]).abs().max()) < 1e-6 * float(b[3].abs().max())
