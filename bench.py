@@ -77,6 +77,9 @@ def main():
     ap.add_argument("--n-mol", type=int, default=343000)
     ap.add_argument("--chunk", type=int, default=131072)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel of known "
+                         "size that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU: the multi-GPU path (spatial domain "
@@ -96,6 +99,7 @@ def main():
     md = MDRunner(model, pos, box, Z, chunk=a.chunk, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device=dev)
     N = md.skin_sys.N
     print(f"# generated {N} atoms (L = {box[0]:.3f} A) in {t_gen:.1f} s; chunk {a.chunk}", file=sys.stderr, flush=True)
+    md.forces()                      # initial forces (set-up: builds the tables and chunk workspaces)
     for i in range(a.warmup):
         md.step()
         print(f"# warmup step {i}: E/N {md.E / N:.6f} eV", file=sys.stderr, flush=True)
@@ -109,6 +113,15 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
+    if a.copy_calib_mib > 0:
+        from mace_onegpu._lib import K, stream
+        n = a.copy_calib_mib << 18
+        src = torch.empty(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        K.mm_fill_f32(src, n, 1.0, stream())      # writes n * 4 bytes
+        torch.mul(src, 2.0, out=dst)              # reads n * 4 bytes, writes n * 4 bytes
+        torch.cuda.synchronize()
+        del src, dst
     n_pairs = int(md.pairs.E)
     value = N * a.steps / dt
     # roofline of the dominant convolution kernel

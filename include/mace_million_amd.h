@@ -92,6 +92,35 @@ int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y,
                  const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                  float* gX, mm_stream_t stream);
 
+/* ---------------------------------------------------------------------------------------------- FusedConvTP
+ * Replace FusedConvTP.forward (fused_conv.py:33-37: the cuEquivariance channelwise-TP polynomial of
+ * fused_edge_conv.path_table, fused_edge_conv.py:43-68) and its autograd backward, with explicit per-edge weights
+ * W [E, nW*128]: out[i] = sum over p in [rowptr[i], rowptr[i+1]) of the TP of edge e = eid[p] (eid null: e = p).
+ * Tables: l1 (nX=1, nW=4, nO=16), l2 (nX=4, nW=10, nO=40), l0123 (nX=16, nW=23, nO=99); Y has 16 components.
+ * Backward: gW [E, nW*128] written; gYp [8][E][16] per-channel-block partial sums of dL/dY (block stride
+ * gy_cb_stride); gX [n, nX*128] accumulated with atomic adds (zero it first); a null output is skipped. */
+int mm_tpw_l1_fwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
+                  const float* W, long w_stride, const float* X, long x_stride, float* out, long out_stride,
+                  mm_stream_t stream);
+int mm_tpw_l2_fwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
+                  const float* W, long w_stride, const float* X, long x_stride, float* out, long out_stride,
+                  mm_stream_t stream);
+int mm_tpw_l0123_fwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
+                     const float* W, long w_stride, const float* X, long x_stride, float* out, long out_stride,
+                     mm_stream_t stream);
+int mm_tpw_l1_bwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
+                  const float* W, long w_stride, const float* X, long x_stride, const float* gO, long g_stride,
+                  float* gW, long gw_stride, float* gYp, long gy_cb_stride, float* gX, long gx_stride,
+                  mm_stream_t stream);
+int mm_tpw_l2_bwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
+                  const float* W, long w_stride, const float* X, long x_stride, const float* gO, long g_stride,
+                  float* gW, long gw_stride, float* gYp, long gy_cb_stride, float* gX, long gx_stride,
+                  mm_stream_t stream);
+int mm_tpw_l0123_bwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
+                     const float* W, long w_stride, const float* X, long x_stride, const float* gO, long g_stride,
+                     float* gW, long gw_stride, float* gYp, long gy_cb_stride, float* gX, long gx_stride,
+                     mm_stream_t stream);
+
 /* ---------------------------------------------------------------------------------------------- (4) node level
  * Symmetric contraction (correlation 3, per species) forward / backward: replaces model.products[k]
  * .symmetric_contractions (graphed_three_pass.py:56-57; cuEquivariance kernel in the reference). */

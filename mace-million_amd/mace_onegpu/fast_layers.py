@@ -319,8 +319,8 @@ class FastLayers:
         ws = self.prepare(g)
         D1 = 4 * C
         h2, gh2, B2, gB2 = ws["h"], ws["gh"], ws["B"], ws["gB"]       # [nC, 128] views of the wider buffers
-        # sc = skip_tp(h1_recv) per species (0e part only), written into h2
-        self._lin(self.plan_sk1, H1x[g.a:g.b], D1, h2, C, self.W_sk1, g.nC, species=True, w_group_stride=1)
+        # sc = skip_tp(h1_recv) per species (0e part only), written into h2; the receivers are g.nodes[:nC]
+        self._lin(self.plan_sk1, H1x, D1, h2, C, self.W_sk1, g.nC, in_rows=g.nodes, species=True, w_group_stride=1)
         # node features of every local node: linear_up(H1x[nodes])
         self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes)
         self._geometry(1, g)
@@ -345,5 +345,5 @@ class FastLayers:
         K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
                        PF[g.e0:g.e1], 0, stream())
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)
-        self._lin(self.plan_sk1, gh2, C, G1[g.a:g.b], D1, self.W_sk1T, g.nC, species=True, w_group_stride=1,
+        self._lin(self.plan_sk1, gh2, C, G1, D1, self.W_sk1T, g.nC, out_rows=g.nodes, species=True, w_group_stride=1,
                   accumulate=1)

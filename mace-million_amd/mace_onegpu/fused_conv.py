@@ -1,0 +1,157 @@
+"""FusedConvTP: gather(sender) -> channelwise tensor product -> scatter_sum(receiver), one HIP kernel each way.
+
+Same module path, class, constructor and forward signature as the reference's mace_onegpu/fused_conv.py:20-37:
+
+    FusedConvTP(segmented_polynomial, weight_numel, irreps_out=None)
+    forward(node_feats [n, nX*128], edge_attrs [E, 16], tp_weights [E, nW*128], edge_index [2, E]) -> [n, nO*128]
+    out[i, o, c] = sum_{e: edge_index[1, e] = i} sum_terms coef * W[e, w, c] * X[edge_index[0, e], k, c] * Y[e, m]
+
+(row 0 of edge_index = sender, row 1 = receiver; rows of nodes that receive no edge are 0; layout ir_mul).
+The reference hands the three inputs to a cuEquivariance SegmentedPolynomial built from
+cue.descriptors.channelwise_tensor_product(...).flatten_coefficient_modes().squeeze_modes()
+(fused_edge_conv.py:43-68); here the descriptor is ChannelwiseTP (the same term list, from
+mace_onegpu.o3.tp_table) and the arithmetic runs in the generated kernels mm_tpw_<table>_{fwd,bwd}
+(receiver-CSR over a stable receiver order, so edges may arrive in any order).  Backward (autograd) gives
+d node_feats (atomic adds on senders), d edge_attrs and d tp_weights.  fp32 only, as the reference's fused
+kernels.
+"""
+import torch
+
+from . import o3
+from ._lib import K, stream
+
+C = 128
+N_CB = 8          # channel blocks of the kernels (one per XCD); the backward returns one dY partial per block
+
+
+class ChannelwiseTP:
+    """Channelwise TP descriptor: node-feature irreps in_ls (C channels each) x spherical harmonics 0..sh_lmax ->
+    mid irreps (l3 in target_ls), e3nn/MACE path order (o3.tp_paths).  Only tables with a compiled kernel
+    (o3.COMPILED_TP_TABLES) can be evaluated."""
+
+    def __init__(self, in_ls, sh_lmax=3, target_ls=(0, 1, 2, 3)):
+        self.in_ls, self.sh_lmax, self.target_ls = tuple(in_ls), int(sh_lmax), tuple(target_ls)
+        self.table = o3.tp_table(list(self.in_ls), self.sh_lmax, self.target_ls)
+        self.name = None
+        for name, key in o3.COMPILED_TP_TABLES.items():
+            if (tuple(key[0]), key[1], tuple(key[2])) == (self.in_ls, self.sh_lmax, self.target_ls):
+                self.name = name
+        t = self.table
+        self.nX, self.nW, self.nO, self.nY = t["nX"], t["nW"], t["nO"], t["nY"]
+        self.weight_numel = self.nW * C
+
+    def require_kernel(self):
+        if self.name is None:
+            raise NotImplementedError(
+                f"no compiled kernel for the channelwise TP {self.in_ls} x Y(l<={self.sh_lmax}) -> {self.target_ls}; "
+                f"compiled tables: {sorted(o3.COMPILED_TP_TABLES)} (add the table to o3.COMPILED_TP_TABLES and "
+                f"rebuild the library)")
+        if self.nY != 16:
+            raise NotImplementedError("the compiled kernels read 16 spherical-harmonic components (l <= 3)")
+        return self.name
+
+    def __repr__(self):
+        return (f"ChannelwiseTP(in_ls={self.in_ls}, sh_lmax={self.sh_lmax}, target_ls={self.target_ls}; nX={self.nX}, "
+                f"nW={self.nW}, nO={self.nO}, terms={len(self.table['terms'])}, kernel={self.name})")
+
+
+def receiver_csr(edge_index, n_nodes, n_send_rows):
+    """(rowptr int32 [n+1], eid int32 [E] or None when already receiver-sorted, send int32 [E]) with bounds checks
+    of both index rows (one device->host read)."""
+    if edge_index.dim() != 2 or edge_index.shape[0] != 2:
+        raise ValueError(f"edge_index must be [2, E], got {tuple(edge_index.shape)}")
+    E = edge_index.shape[1]
+    if E >= 2 ** 31:
+        raise ValueError("more than 2^31 - 1 edges")
+    dev = edge_index.device
+    send = edge_index[0].to(torch.int32).contiguous()
+    recv = edge_index[1].long()
+    if E == 0:
+        return torch.zeros(n_nodes + 1, dtype=torch.int32, device=dev), None, send
+    stats = torch.stack([send.min().long(), send.max().long(), recv.min(), recv.max(),
+                         (recv[1:] >= recv[:-1]).all().long() if E > 1 else torch.ones((), dtype=torch.long,
+                                                                                        device=dev)]).tolist()
+    smin, smax, rmin, rmax, is_sorted = stats
+    if smin < 0 or smax >= n_send_rows:
+        raise IndexError(f"sender index out of range [0, {n_send_rows}): min {smin}, max {smax}")
+    if rmin < 0 or rmax >= n_nodes:
+        raise IndexError(f"receiver index out of range [0, {n_nodes}): min {rmin}, max {rmax}")
+    counts = torch.bincount(recv, minlength=n_nodes)
+    rowptr = torch.zeros(n_nodes + 1, dtype=torch.int64, device=dev)
+    torch.cumsum(counts, 0, out=rowptr[1:])
+    eid = None if is_sorted else torch.argsort(recv, stable=True).to(torch.int32)
+    return rowptr.to(torch.int32), eid, send
+
+
+def _check(t, name, cols):
+    if not t.is_cuda:
+        raise TypeError(f"{name} must be a GPU tensor")
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 (the fused kernels are fp32), got {t.dtype}")
+    if t.dim() != 2 or t.shape[1] != cols:
+        raise ValueError(f"{name} must be [rows, {cols}], got {tuple(t.shape)}")
+    return t.contiguous()
+
+
+class _FusedConvFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, X, Y, W, edge_index, desc):
+        name = desc.require_kernel()
+        X = _check(X, "node_feats", desc.nX * C)
+        Y = _check(Y, "edge_attrs", desc.nY)
+        W = _check(W, "tp_weights", desc.nW * C)
+        E = edge_index.shape[1]
+        if Y.shape[0] != E or W.shape[0] != E:
+            raise ValueError(f"edge_attrs / tp_weights rows ({Y.shape[0]}, {W.shape[0]}) != number of edges {E}")
+        n = X.shape[0]
+        rowptr, eid, send = receiver_csr(edge_index, n, n)
+        out = torch.empty(n, desc.nO * C, dtype=torch.float32, device=X.device)
+        getattr(K, f"mm_tpw_{name}_fwd")(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X, X.stride(0), out,
+                                         out.stride(0), stream())
+        ctx.save_for_backward(X, Y, W, rowptr, send, eid if eid is not None else torch.empty(0))
+        ctx.has_eid = eid is not None
+        ctx.desc = desc
+        return out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, gO):
+        X, Y, W, rowptr, send, eid = ctx.saved_tensors
+        eid = eid if ctx.has_eid else None
+        desc = ctx.desc
+        gO = gO.contiguous()
+        n, E = X.shape[0], Y.shape[0]
+        nx, ny, nw = ctx.needs_input_grad[:3]
+        gX = torch.zeros_like(X) if nx else None
+        gYp = torch.empty(N_CB, E, 16, dtype=torch.float32, device=X.device) if (ny and E) else None
+        gW = torch.empty_like(W) if nw else None
+        if E and (nx or ny or nw):
+            getattr(K, f"mm_tpw_{desc.name}_bwd")(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X,
+                                                  X.stride(0), gO, gO.stride(0), gW, W.stride(0), gYp, E * 16, gX,
+                                                  X.stride(0), stream())
+        gY = None
+        if ny:
+            gY = gYp.sum(0) if E else torch.zeros_like(Y)
+        if nw and not E:
+            gW = torch.zeros_like(W)
+        return gX, gY, gW, None, None
+
+
+class FusedConvTP(torch.nn.Module):
+    """gather(sender) -> channelwise tensor product -> scatter_add(receiver), fused in one HIP kernel.
+
+    forward(node_feats [n_nodes, in1], edge_attrs [E, in2], tp_weights [E, W], edge_index [2, E]) -> [n_nodes, out]
+    m_ji is never materialised: output rows are accumulated on the receiver inside the kernel."""
+
+    def __init__(self, segmented_polynomial, weight_numel, irreps_out=None):
+        super().__init__()
+        if not isinstance(segmented_polynomial, ChannelwiseTP):
+            raise TypeError("segmented_polynomial must be a mace_onegpu.fused_conv.ChannelwiseTP descriptor")
+        self.m = segmented_polynomial
+        self.weight_numel = int(weight_numel)
+        if self.weight_numel != self.m.weight_numel:
+            raise ValueError(f"weight_numel {self.weight_numel} != {self.m.weight_numel} of the descriptor")
+        self.irreps_out = irreps_out
+
+    def forward(self, node_feats, edge_attrs, tp_weights, edge_index):
+        return _FusedConvFn.apply(node_feats, edge_attrs, tp_weights, edge_index, self.m)

@@ -7,9 +7,11 @@ mace_onegpu/mliap_threepass.py (ThreePassMLIAP, :155-622):
     pass B  chunks: E2 = layer-2 energy;  dE2/drij -> pair forces,  dE2/dh1 -> G1[local + ghost]
             reverse_exchange(G1)                                                        -> ghost terms on owners
     pass C  chunks: layer 1 again with gradient; loss = scale R1 + G1 . h1; d/drij -> pair forces
-Only H1, G1 and per-pair arrays persist; every wide intermediate lives in one chunk's workspace.
-The arithmetic runs in the HIP kernels of libmace_million_amd.so (fast_layers.FastLayers); full chunks can be
-captured once as HIP graphs (MACE3P_GRAPHS=1) and replayed per chunk.
+H1, G1, the per-pair arrays and (MACE3P_CACHE_L1=1, the default) pass A's layer-1 message and density of every
+local atom (8 KiB per atom, so that pass C does not recompute layer 1) persist; every other wide intermediate lives
+in one chunk's workspace.  The arithmetic runs in the HIP kernels of libmace_million_amd.so
+(fast_layers.FastLayers); with MACE3P_GRAPHS=1 the passes of full chunks are captured once as HIP graphs and
+replayed per chunk (chunk_graphs.ChunkGraphExec).
 """
 import json
 import os
@@ -17,7 +19,7 @@ import time
 
 import torch
 
-from . import fast_layers
+from . import chunk_graphs, fast_layers
 from .receiver_chunk_mace import chunk_topology, make_chunk
 
 try:
@@ -110,6 +112,28 @@ class ThreePassMLIAP(MLIAPUnified):
         path = os.environ.get("MACE3P_LOG")
         self._log = open(path, "a", buffering=1) if path else None
 
+    def _prepare_graphs(self, graphs, nt):
+        """A captured executor that fits every full chunk of this call (recaptured when a capacity is exceeded);
+        None without full chunks (mliap_threepass.py:390-431)."""
+        full = [g for g in graphs if g.nC == self.chunk]
+        if not full:
+            return None
+        n_max = max(g.n_nodes for g in full)
+        e_max = max(g.nE for g in full)
+        gx = self._gx
+        if gx is None or gx.cache_layer1 != self._cache_l1 or not gx.fits(n_max, e_max, nt):
+            self._gx = gx = None
+            torch.cuda.empty_cache()
+            margin = float(os.environ.get("MACE3P_CAP_MARGIN", "1.25"))
+            n_cap, e_cap, nt_cap = chunk_graphs.capacities(n_max, e_max, nt, self.e_align, margin)
+            gx = chunk_graphs.ChunkGraphExec(self._fl, self.chunk, n_cap, e_cap, nt_cap, "rij", self._cache_l1)
+            gx.capture(full[0])
+            self._gx = gx
+            self.n_captures = getattr(self, "n_captures", 0) + 1
+            if self._log is not None:
+                self._log.write(json.dumps(dict(capture=dict(n_cap=n_cap, e_cap=e_cap, nt_cap=nt_cap))) + "\n")
+        return gx
+
     def _topology_all(self, bounds, rp_cpu, pi, pj, nl, nt):
         """{(a, b): (nodes int32, local sender index int32 [nE])} for every receiver chunk, identical to
         ThreePassMLIAP._topology chunk by chunk (mliap_threepass.py:288-310, :344-388)."""
@@ -165,6 +189,7 @@ class ThreePassMLIAP(MLIAPUnified):
             g = make_chunk(a, b, e0, e1, topo[(a, b)][0], topo[(a, b)][1], rp, node_spec_all)
             g.rij, g.pair_i = rij[e0:e1], pi[e0:e1]
             graphs.append(g)
+        gx = self._prepare_graphs(graphs, nt) if self._use_graphs else None
         torch.cuda.synchronize()
         t["A_topology"] = time.perf_counter() - t0
         eat = torch.zeros(nl, dtype=torch.float64, device=dev)
@@ -178,19 +203,29 @@ class ThreePassMLIAP(MLIAPUnified):
                 self._l1cache = fl.layer1_cache(nl)
             cache = self._l1cache
         for g in graphs:
-            fl.pass_a(g, H1, cache)
-        H1x = torch.empty_like(H1)
+            if gx is not None and g.nC == C:
+                gx.pass_a(g, H1, cache)
+            else:
+                fl.pass_a(g, H1, cache)
+        H1x = gx.H1x[:nt] if gx is not None else torch.empty_like(H1)
         _exchange(data.forward_exchange, H1, H1x, D1)
         del H1
         torch.cuda.synchronize()
         t["A"] = time.perf_counter() - t0
         # ---------------- pass B
         t0 = time.perf_counter()
-        G1 = torch.zeros_like(H1x)
+        if gx is not None:
+            G1 = gx.G1[:nt]
+            G1.zero_()
+        else:
+            G1 = torch.zeros_like(H1x)
         for g in graphs:
-            fl.pass_b(g, H1x, G1, PF, eat)
-        if cache is None:
-            del H1x
+            if gx is not None and g.nC == C:
+                gx.pass_b(g, PF, eat)
+            else:
+                fl.pass_b(g, H1x, G1, PF, eat)
+        H1c = H1x if cache is not None else None       # pass C reads h1 from H1x only with the layer-1 cache
+        del H1x
         G1r = torch.empty_like(G1)
         _exchange(data.reverse_exchange, G1, G1r, D1)
         del G1
@@ -199,11 +234,13 @@ class ThreePassMLIAP(MLIAPUnified):
         # ---------------- pass C
         t0 = time.perf_counter()
         for g in graphs:
-            if cache is None:
+            if gx is not None and g.nC == C:
+                gx.pass_c(g, G1r, PF, eat, H1c, cache)
+            elif cache is None:
                 fl.pass_c(g, G1r, PF, eat)
             else:
-                fl.pass_c(g, G1r, PF, eat, H1x, cache)
-        del G1r
+                fl.pass_c(g, G1r, PF, eat, H1c, cache)
+        del G1r, H1c
         torch.cuda.synchronize()
         t["C"] = time.perf_counter() - t0
         eat += self._e0[elems[:nl]] + self.shift

@@ -206,6 +206,14 @@ def tp_table(in_ls, sh_lmax=LMAX_SH, target_ls=(0, 1, 2, 3), tol=1e-12):
                 mid_ls=mid.ls, in_ls=list(in_ls))
 
 
+# Channelwise-TP path tables that have a compiled explicit-weight kernel (mm_tpw_<name>_{fwd,bwd}, used by
+# FusedConvTP): name -> (node-feature ls, SH lmax, target ls).  The two interaction blocks of the MACE-MPA-0
+# architecture and the full l<=3 table (node features 0e+1o+2e+3o) of the edge-convolution microbenchmark.
+COMPILED_TP_TABLES = {"l1": ((0,), 3, (0, 1, 2, 3)),
+                      "l2": ((0, 1), 3, (0, 1, 2, 3)),
+                      "l0123": ((0, 1, 2, 3), 3, (0, 1, 2, 3))}
+
+
 # ----------------------------------------------------------------------------- symmetric contraction paths
 def _sym_monomials(nvar, deg):
     """All sorted index tuples (i1 <= ... <= i_deg) -> position."""

@@ -137,7 +137,8 @@ def make_chunk(a, b, e0, e1, nodes, ls, rowptr_full, node_spec_all):
 class ReceiverChunkMACE:
     """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
 
-    def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True):
+    def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True, use_graphs=False,
+                 e_align=65536):
         self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
         self.dev = torch.device(device)
         self.fl = None
@@ -145,6 +146,10 @@ class ReceiverChunkMACE:
         # keep pass A's layer-1 message and density (8 KiB per atom) so that pass C does not recompute them
         self.cache_layer1 = bool(cache_layer1)
         self._cache = None
+        # full chunks replayed from HIP graphs (chunk_graphs.ChunkGraphExec), recaptured when a capacity is exceeded
+        self.use_graphs, self.e_align = bool(use_graphs), int(e_align)
+        self._gx = None
+        self.n_captures = 0
 
     def _layers(self, sysm):
         from .fast_layers import FastLayers
@@ -175,6 +180,29 @@ class ReceiverChunkMACE:
             out.append(g)
         return out
 
+    def _graph_exec(self, fl, sysm, graphs):
+        from . import chunk_graphs
+        full = [g for g in graphs if g.nC == self.chunk]
+        if not full:
+            return None
+        n_max = max(g.n_nodes for g in full)
+        e_max = max(g.nE for g in full)
+        box = tuple(float(b) for b in sysm.box)
+        gx = self._gx
+        if gx is None or gx.box != box or not gx.fits(n_max, e_max, sysm.N):
+            self._gx = gx = None
+            torch.cuda.empty_cache()
+            n_cap, e_cap, nt_cap = chunk_graphs.capacities(n_max, e_max, sysm.N, self.e_align)
+            gx = chunk_graphs.ChunkGraphExec(fl, self.chunk, n_cap, e_cap, nt_cap, "pos", self.cache_layer1,
+                                             box_host=host_f64(box))
+            gx.box = box
+            gx.set_positions(sysm.pos)
+            gx.capture(full[0])
+            self._gx = gx
+            self.n_captures += 1
+        gx.set_positions(sysm.pos)
+        return gx
+
     def compute(self, sysm, graphs=None, timings=None):
         """Returns (E float, eat fp64 [N], F fp64 [N, 3], PF fp32 [E, 3]) in the sorted index space."""
         fl = self._layers(sysm)
@@ -184,27 +212,45 @@ class ReceiverChunkMACE:
         t = {}
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        H1 = torch.zeros(N, self.D1, dtype=torch.float32, device=dev)
+        gx = self._graph_exec(fl, sysm, graphs) if self.use_graphs else None
+        nC = self.chunk
+        if gx is not None:
+            H1, G1 = gx.H1x[:N], gx.G1[:N]
+            H1.zero_()
+        else:
+            H1 = torch.zeros(N, self.D1, dtype=torch.float32, device=dev)
         cache = None
         if self.cache_layer1:
             if self._cache is None or self._cache["rho"].numel() < N:
                 self._cache = fl.layer1_cache(N)
             cache = self._cache
         for g in graphs:
-            fl.pass_a(g, H1, cache)
+            if gx is not None and g.nC == nC:
+                gx.pass_a(g, H1, cache)
+            else:
+                fl.pass_a(g, H1, cache)
         torch.cuda.synchronize()
         t["A"] = time.perf_counter() - t0
         t0 = time.perf_counter()
-        G1 = torch.zeros_like(H1)
+        if gx is not None:
+            G1.zero_()
+        else:
+            G1 = torch.zeros_like(H1)
         PF = torch.zeros(max(E, 1), 3, dtype=torch.float32, device=dev)
         eat = torch.zeros(N, dtype=torch.float64, device=dev)
         for g in graphs:
-            fl.pass_b(g, H1, G1, PF, eat)
+            if gx is not None and g.nC == nC:
+                gx.pass_b(g, PF, eat)
+            else:
+                fl.pass_b(g, H1, G1, PF, eat)
         torch.cuda.synchronize()
         t["B"] = time.perf_counter() - t0
         t0 = time.perf_counter()
         for g in graphs:
-            fl.pass_c(g, G1, PF, eat, H1, cache)
+            if gx is not None and g.nC == nC:
+                gx.pass_c(g, G1, PF, eat, H1, cache)
+            else:
+                fl.pass_c(g, G1, PF, eat, H1, cache)
         torch.cuda.synchronize()
         t["C"] = time.perf_counter() - t0
         eat += fl.e0[sysm.spidx.long()] + fl.shift
