@@ -43,6 +43,34 @@ def conv_algorithmic(name, E, nC, N, tab):
     return B, F
 
 
+def kernel_sources_digest():
+    """sha256 over the HIP sources of the library (csrc/ and csrc/gen/), to tie measurements to the kernels."""
+    import hashlib
+    h = hashlib.sha256()
+    base = os.path.join(ROOT, "mace-million_amd", "csrc")
+    for d in (base, os.path.join(base, "gen")):
+        for f in sorted(os.listdir(d)):
+            if f.endswith((".hip", ".h", ".cpp")):
+                with open(os.path.join(d, f), "rb") as fh:
+                    h.update(f.encode() + fh.read())
+    return h.hexdigest()
+
+
+def measured_traffic(kernel, n_mol, chunk):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this
+    workload (profiles/traffic_config5_water1M.json: counters scaled by a copy kernel of known size), or None
+    when no pass was recorded for this workload and these kernel sources."""
+    path = os.path.join(ROOT, "profiles", "traffic_config5_water1M.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as fh:
+        t = json.load(fh)
+    if (t["workload"] != {"n_mol": n_mol, "chunk": chunk} or kernel not in t["kernels"]
+            or t.get("kernel_sources_sha256") != kernel_sources_digest()):
+        return None
+    return t["kernels"][kernel]["traffic_bytes_per_launch"]
+
+
 def cpu_baseline(seed=0):
     """fp64 CPU oracle, one full E+F of a 512-molecule box from the same generator."""
     import torch
@@ -140,7 +168,8 @@ def main():
     if dom:
         k = kernels[dom]
         roof = {"kernel": f"mm_{dom}_kernel", "bound": "hbm", "achieved": round(k["GBps"], 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(k["hbm_frac"], 5), "traffic": None,
+                "unit": "GB/s", "frac": round(k["hbm_frac"], 5),
+                "traffic": measured_traffic(f"mm_{dom}_kernel", a.n_mol, a.chunk),
                 "flop_rate_TFLOPs": round(k["TFLOPs"], 3), "valu_frac": round(k["valu_frac"], 4),
                 "bytes_per_launch": int(k["bytes_per_launch"]), "ms_per_launch": round(k["ms_per_launch"], 4),
                 "launches": k["launches"]}
@@ -155,6 +184,7 @@ def main():
         "config": {"workload": "config5: 343,000-molecule water (1,029,000 atoms), random-init MPA-0-medium "
                                "architecture, velocity-Verlet MD dt 0.5 fs, skin 2 A",
                    "atoms": N, "pairs": n_pairs, "chunk": a.chunk, "rebuilds_timed": md.n_rebuild - rebuilds0,
+                   "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2),
                    "box_A": round(float(box[0]), 4)},
         "roofline": roof,
         "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}

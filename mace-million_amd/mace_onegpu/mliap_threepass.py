@@ -75,19 +75,34 @@ class ThreePassMLIAP(MLIAPUnified):
         self.e_align = int(e_align)
         self.dtype = next(model.parameters()).dtype
         self.step = 0
-        self._rebuild = None if rebuild_config is None else rebuild_config
+        # rebuild recipe (class, constructor kwargs, state_dict): the file then stores no module object and the
+        # model is constructed again on the first force call (mliap_threepass.py:172-202)
+        self._rebuild = None
+        if rebuild_config is not None:
+            self._rebuild = (type(model), dict(rebuild_config),
+                             {k: v.detach().cpu() for k, v in model.state_dict().items()})
 
     # runtime objects (device tables, kernels' constants, graphs) are rebuilt after unpickling
     def __getstate__(self):
         d = self.__dict__.copy()
         for k in _RUNTIME:
             d.pop(k, None)
+        if d.get("_rebuild") is not None:
+            d.pop("model", None)
         return d
+
+    def _rebuild_model(self):
+        cls, cfg, sd = self._rebuild
+        m = cls(**cfg)
+        m.load_state_dict(sd, strict=True)
+        return m.to(self.dtype)
 
     # ------------------------------------------------------------------ setup
     def _setup(self, elems):
         dev = elems.device if elems.is_cuda else torch.device("cuda")
         self._dev = dev
+        if getattr(self, "model", None) is None:
+            self.model = self._rebuild_model()
         if os.environ.get("MACE3P_CHUNK"):
             self.chunk = int(os.environ["MACE3P_CHUNK"])
         self.model = self.model.to(dev).eval()

@@ -76,6 +76,29 @@ def test_neighbor_list_large_box_matches_oracle(dev):
     assert np.array_equal(s.send.cpu().numpy(), send)
 
 
+@pytest.mark.parametrize("case", ["water98304", "fcc500000"])
+def test_neighbor_list_full_size_matches_c_oracle(dev, case):
+    """Bit-exact at BASELINE sizes: config 3's 98,304-atom water box and config 4's 500,000-atom FCC alloy
+    (GPU cell list vs the plain-C restatement of the reference's build)."""
+    from mace_onegpu import systems
+    from mace_onegpu.receiver_chunk_mace import System
+    from oracle import nlist_c
+    _say(f"case {case}")
+    if case == "water98304":
+        pos, box, Z = systems.water_box(32768, seed=0)
+    else:
+        pos, box, Z = systems.fcc_alloy(n_cells=50)
+    s = System(pos, box, np.zeros(len(pos), np.int32), 6.0, dev)
+    s.build_neighbors()
+    perm, pos_sorted, NN, rowptr, send = nlist_c.neighbor_list(pos, box, 6.0)
+    _say(f"  {len(pos)} atoms, {len(send)} pairs")
+    assert np.array_equal(s.perm.cpu().numpy(), perm)
+    assert np.array_equal(s.pos.cpu().numpy(), pos_sorted)
+    assert np.array_equal(s.NN.cpu().numpy(), NN)
+    assert np.array_equal(s.rowptr.cpu().numpy(), rowptr)
+    assert np.array_equal(s.send.cpu().numpy(), send)
+
+
 # ----------------------------------------------------------------------------- kernels
 def test_mfma_linear_against_torch(dev):
     """mm_linear: several K-chunks, row gathers/scatters, species lists, 1/(rho+1) scaling, accumulate."""

@@ -37,6 +37,33 @@ def test_oracle_neighbors_equal_brute_force_set(name):
     assert got == neighbors.brute_force_pairs(s.pos, s.box, 6.0)
 
 
+@pytest.mark.parametrize("name", CASES)
+def test_c_oracle_neighbors_bit_exact_with_reference(name):
+    """The plain-C restatement (oracle/nlist_c) reproduces the reference's golden neighbour lists."""
+    from oracle import nlist_c
+    g = golden(name)
+    perm, pos_sorted, NN, rowptr, send = nlist_c.neighbor_list(g["pos"], g["box"], 6.0)
+    assert np.array_equal(perm, g["perm"])
+    assert np.array_equal(pos_sorted, g["pos_sorted"])
+    assert np.array_equal(NN, g["NN"])
+    assert np.array_equal(send, g["send"])
+
+
+def test_c_oracle_equals_numpy_oracle_on_a_larger_box():
+    """C and numpy restatements agree on a 3,000-atom random box with ties at the cutoff and atoms on cell faces."""
+    from oracle import nlist_c
+    rng = np.random.default_rng(11)
+    box = np.array([21.0, 19.5, 24.25])
+    pos = rng.uniform(-5.0, 30.0, size=(3000, 3))
+    pos[:40] = np.round(pos[:40])                       # lattice points: exact 6.0 A separations exist
+    pos[40:60, 0] = 6.5                                 # on a cell face (box / ncell = 7.0 ... 6.5)
+    s = neighbors.SystemRef(pos, box, np.zeros(3000, int), 6.0)
+    NN0, rp0, send0 = s.build_neighbors()
+    perm, pos_sorted, NN, rowptr, send = nlist_c.neighbor_list(pos, box, 6.0)
+    assert np.array_equal(perm, s.perm) and np.array_equal(pos_sorted, s.pos)
+    assert np.array_equal(NN, NN0) and np.array_equal(rowptr, rp0) and np.array_equal(send, send0)
+
+
 T = np.load(os.path.join(HERE, "golden", "topology.npz"))
 
 
