@@ -57,23 +57,22 @@ int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] *
 
 /* ---------------------------------------------------------------------------------------------- edge geometry
  * Replace receiver_chunk_mace.edge_embed (:230-234), the table coordinates of spline_w._coords (spline_w.py:18-27)
- * and the density part of FastLayers.layer1/layer2_energy (fast_layers.py:179-183, 190-192, 209-213): Y_lm l<=3,
- * local receiver, and a packed float4 per edge (t, spline interval row of the ordered species pair's table,
- * sender feature row (its species when x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).
- * dens_w is HOST [nb]. */
+ * and the density part of FastLayers.layer1/layer2_energy (fast_layers.py:179-183, 190-192, 209-213): per edge
+ * e_u float4 (unit vector, length; the convolutions evaluate Y_lm l<=3 from it), the local receiver, and a packed
+ * float4 (t, spline interval row of the ordered species pair's table, sender feature row (its species when
+ * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).  dens_w is HOST [nb]. */
 int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* local_send,
                      const int* node_spec, int S, const int* pair_map, const float* dens_w, int nb, float r_max,
-                     int p_cut, int M, float r_lo, float inv_h, int x_from_spec, float* e_vec, float* e_Y,
-                     float* e_pk, int* e_recv, float* e_dd, mm_stream_t stream);
+                     int p_cut, int M, float r_lo, float inv_h, int x_from_spec, float* e_u, float* e_pk,
+                     int* e_recv, float* e_dd, mm_stream_t stream);
 int mm_edge_geom_pos(int E, const double* pos, const double* box /* HOST [3] */, const int* recv_local, int a,
                      const int* local_send, const int* nodes, const int* node_spec, int S, const int* pair_map,
                      const float* dens_w, int nb, float r_max, int p_cut, int M, float r_lo, float inv_h,
-                     int x_from_spec, float* e_vec, float* e_Y, float* e_pk, int* e_recv, float* e_dd,
-                     mm_stream_t stream);
+                     int x_from_spec, float* e_u, float* e_pk, int* e_recv, float* e_dd, mm_stream_t stream);
 /* per-edge dL/dv from the convolution backward partials, the density term and the SH chain rule (the autograd
  * step torch.autograd.grad(..., [vec]) of mliap_threepass.py:550, 580) */
 int mm_edge_grad(int E, const float* part, long part_stride, int n_part, const float* g_rho, const int* e_recv,
-                 const float* e_dd, const float* e_vec, float* pair_force, int accumulate, mm_stream_t stream);
+                 const float* e_dd, const float* e_u, float* pair_force, int accumulate, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- (2)+(3) edge conv
  * Replace conv_spline.ConvSpline.forward / gen_fwd (conv_spline.py:38-94, 294-301), spline_w._w_fwd
@@ -81,14 +80,14 @@ int mm_edge_grad(int E, const float* part, long part_stride, int n_part, const f
  * receiver-CSR sum; and their backward (conv_spline.gen_bwd :97-181, spline_w._w_bwd :53-75): per-edge
  * dL/dr, dL/dY partials per channel block, optional dL/dX (layer 2, G1 path).  tab: interval coefficients built by
  * mm_spline_coeffs.  Layer 1: nX=1, nW=4, nO=16; layer 2: nX=4, nW=10, nO=40. */
-int mm_conv1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* X, int x_stride,
+int mm_conv1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float* out, float* rho, mm_stream_t stream);
-int mm_conv2_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* X, int x_stride,
+int mm_conv2_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float* out, float* rho, mm_stream_t stream);
-int mm_conv1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* X, int x_stride,
+int mm_conv1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                  float* gX, mm_stream_t stream);
-int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* X, int x_stride,
+int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                  float* gX, mm_stream_t stream);
 

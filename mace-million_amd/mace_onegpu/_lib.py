@@ -36,8 +36,8 @@ SIGNATURES = {
     "mm_nl_filter_count": [P, L, P, P, P, D, P, P],
     "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P],
     # geometry
-    "mm_edge_geom_rij": [I, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
-    "mm_edge_geom_pos": [I, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
+    "mm_edge_geom_rij": [I, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P],
+    "mm_edge_geom_pos": [I, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P],
     "mm_edge_grad": [I, P, L, I, P, P, P, P, P, I, P],
     # convolutions (generated)
     "mm_conv1_fwd": [P, I, P, P, P, I, P, I, I, P, P, P],

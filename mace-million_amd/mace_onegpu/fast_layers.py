@@ -219,7 +219,7 @@ class FastLayers:
         f = dict(dtype=torch.float32, device=dev)
         i = dict(dtype=torch.int32, device=dev)
         ws = dict(nC=nC, nN=n_nodes, E=E)
-        ws.update(e_vec=torch.empty(E, 3, **f), e_Y=torch.empty(E, 16, **f), e_pk=torch.empty(E, 4, **f),
+        ws.update(e_u=torch.empty(E, 4, **f), e_pk=torch.empty(E, 4, **f),
                   e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
         ws.update(spec=torch.empty(n_nodes, **i), lists=torch.empty(self.S * nC, **i), counts=torch.empty(self.S, **i))
         ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
@@ -251,11 +251,11 @@ class FastLayers:
         if g.rij is not None:
             K.mm_edge_geom_rij(g.nE, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
                                sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo, self.inv_h, x_from_spec,
-                               ws["e_vec"], ws["e_Y"], ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
+                               ws["e_u"], ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
         else:
             K.mm_edge_geom_pos(g.nE, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
                                self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo,
-                               self.inv_h, x_from_spec, ws["e_vec"], ws["e_Y"], ws["e_pk"], ws["e_recv"],
+                               self.inv_h, x_from_spec, ws["e_u"], ws["e_pk"], ws["e_recv"],
                                ws["e_dd"], stream())
 
     def prepare(self, g):
@@ -271,7 +271,7 @@ class FastLayers:
         contraction input) and the density."""
         ws = self.ws
         self._geometry(0, g)
-        self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+        self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                     self.Xs1, C, self.tab[0], self.n_tab, self.M, ws["A"], rho_out, stream())
         self._lin(self.plan_l1, ws["A"], 16 * C, M_out, 16 * C, self.W_l1, g.nC, scale=rho_out, scale_mode=1,
                   species=True, w_group_stride=4)
@@ -306,10 +306,10 @@ class FastLayers:
                        stream())
         self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=rho, scale_mode=1,
                   species=True, w_group_stride=4)
-        self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+        self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                     self.Xs1, C, self.tab[0], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17,
                     None, stream())
-        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
+        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
                        PF[g.e0:g.e1], 1, stream())
 
     # ------------------------------------------------------------------ layer 2
@@ -324,7 +324,7 @@ class FastLayers:
         # node features of every local node: linear_up(H1x[nodes])
         self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes)
         self._geometry(1, g)
-        self._timed("conv2_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+        self._timed("conv2_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                     ws["Xh"], D1, self.tab[1], self.n_tab, self.M, ws["A"], ws["rho"], stream())
         self._lin(self.plan_lin2, ws["A"], self.nO2 * C, ws["M"], 16 * C, self.W_lin2, g.nC, scale=ws["rho"],
                   scale_mode=1)
@@ -339,10 +339,10 @@ class FastLayers:
         self._lin(self.plan_lin2T, ws["gM"], 16 * C, ws["gA"], self.nO2 * C, self.W_lin2T, g.nC, scale=ws["rho"],
                   scale_mode=1)
         K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
-        self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+        self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                     ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17,
                     ws["gXh"], stream())
-        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_vec"],
+        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
                        PF[g.e0:g.e1], 0, stream())
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)
         self._lin(self.plan_sk1, gh2, C, G1, D1, self.W_sk1T, g.nC, out_rows=g.nodes, species=True, w_group_stride=1,
