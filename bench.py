@@ -28,10 +28,18 @@ VALU_F32_PEAK_TFLOPS = 78.6      # fp32 vector FMA without packed-FP32 instructi
 MFMA_F32_PEAK_TFLOPS = 157.3
 
 
-def conv_algorithmic(name, E, nC, N, tab):
+def conv_algorithmic(name, E, nC, N, tab, Kp=128):
     """Algorithmic HBM bytes and FLOPs of one convolution launch (per-edge, per-receiver and per-node terms;
-    tables read once).  P = distinct tables (1: this model's radial weights do not depend on the species)."""
+    tables read once).  P = distinct tables (1: this model's radial weights do not depend on the species).
+    ace1_*: layer 1 in the density-projection form -- per edge the 16 B record and 16 harmonics (fwd; bwd also
+    writes 17 floats), the 64-feature table once, B / gB [nC, 16, Kp] once; FLOPs = the 64 x 16 outer product
+    (fwd) or its two transposed products (bwd) plus the spline evaluation."""
     C, P, M = 128, 1, 512
+    if name.startswith("ace1"):
+        tab_bytes = 16 * (M - 1) * 64
+        if name == "ace1_fwd":
+            return 80 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp + 4 * nC, 2 * E * 64 * 16 + 6 * E * 64
+        return 148 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp, 4 * E * 64 * 16 + 10 * E * 64
     nX, nW, nO, nT = tab["nX"], tab["nW"], tab["nO"], len(tab["terms"])
     gx = 1 if name == "conv2_bwd" else 0
     if name.endswith("fwd"):
@@ -156,13 +164,18 @@ def main():
     kernels = {}
     for name, d in ktimes.items():
         tab = fl.tables.tp1 if name.startswith("conv1") else fl.tables.tp2
-        B = sum(conv_algorithmic(name, *u, tab)[0] for u in d["units"])
-        F = sum(conv_algorithmic(name, *u, tab)[1] for u in d["units"])
+        Kp = getattr(fl, "ace_Kp", 128)
+        B = sum(conv_algorithmic(name, *u, tab, Kp)[0] for u in d["units"])
+        F = sum(conv_algorithmic(name, *u, tab, Kp)[1] for u in d["units"])
         sec = d["ms_total"] * 1e-3
         kernels[name] = dict(launches=d["launches"], ms_per_launch=d["ms_total"] / d["launches"],
                              ms_per_step=d["ms_total"] / a.steps, GBps=B / sec / 1e9, TFLOPs=F / sec / 1e12,
-                             hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS, valu_frac=F / sec / 1e12 / VALU_F32_PEAK_TFLOPS,
+                             hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS,
                              bytes_per_launch=B / d["launches"], flops_per_launch=F / d["launches"])
+        if name.startswith("ace1"):      # the edge products run on MFMA
+            kernels[name]["mfma_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
+        else:
+            kernels[name]["valu_frac"] = F / sec / 1e12 / VALU_F32_PEAK_TFLOPS
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"]) if kernels else None
     roof = None
     if dom:
@@ -170,7 +183,8 @@ def main():
         roof = {"kernel": f"mm_{dom}_kernel", "bound": "hbm", "achieved": round(k["GBps"], 2), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(k["hbm_frac"], 5),
                 "traffic": measured_traffic(f"mm_{dom}_kernel", a.n_mol, a.chunk),
-                "flop_rate_TFLOPs": round(k["TFLOPs"], 3), "valu_frac": round(k["valu_frac"], 4),
+                "flop_rate_TFLOPs": round(k["TFLOPs"], 3),
+                **{f: round(k[f], 4) for f in ("valu_frac", "mfma_frac") if f in k},
                 "bytes_per_launch": int(k["bytes_per_launch"]), "ms_per_launch": round(k["ms_per_launch"], 4),
                 "launches": k["launches"]}
     cpu = None

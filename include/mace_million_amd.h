@@ -58,17 +58,19 @@ int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] *
 /* ---------------------------------------------------------------------------------------------- edge geometry
  * Replace receiver_chunk_mace.edge_embed (:230-234), the table coordinates of spline_w._coords (spline_w.py:18-27)
  * and the density part of FastLayers.layer1/layer2_energy (fast_layers.py:179-183, 190-192, 209-213): per edge
- * e_u float4 (unit vector, length; the convolutions evaluate Y_lm l<=3 from it), the local receiver, and a packed
+ * e_u float4 (unit vector, length; the convolutions evaluate Y_lm l<=3 from it), optionally the 16 harmonics e_Y
+ * (for the layer-1 ACE kernels), the local receiver, and a packed
  * float4 (t, spline interval row of the ordered species pair's table, sender feature row (its species when
  * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).  dens_w is HOST [nb]. */
 int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* local_send,
                      const int* node_spec, int S, const int* pair_map, const float* dens_w, int nb, float r_max,
-                     int p_cut, int M, float r_lo, float inv_h, int x_from_spec, float* e_u, float* e_pk,
-                     int* e_recv, float* e_dd, mm_stream_t stream);
+                     int p_cut, int M, float r_lo, float inv_h, int x_from_spec, float* e_u, float* e_Y /* nullable */,
+                     float* e_pk, int* e_recv, float* e_dd, mm_stream_t stream);
 int mm_edge_geom_pos(int E, const double* pos, const double* box /* HOST [3] */, const int* recv_local, int a,
                      const int* local_send, const int* nodes, const int* node_spec, int S, const int* pair_map,
                      const float* dens_w, int nb, float r_max, int p_cut, int M, float r_lo, float inv_h,
-                     int x_from_spec, float* e_u, float* e_pk, int* e_recv, float* e_dd, mm_stream_t stream);
+                     int x_from_spec, float* e_u, float* e_Y /* nullable */, float* e_pk, int* e_recv, float* e_dd,
+                     mm_stream_t stream);
 /* per-edge dL/dv from the convolution backward partials, the density term and the SH chain rule (the autograd
  * step torch.autograd.grad(..., [vec]) of mliap_threepass.py:550, 580) */
 int mm_edge_grad(int E, const float* part, long part_stride, int n_part, const float* g_rho, const int* e_recv,
@@ -90,6 +92,21 @@ int mm_conv1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u,
 int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                  float* gX, mm_stream_t stream);
+
+/* ---------------------------------------------------------------------------------------------- layer-1 ACE form
+ * Replace ace_layer1.ACELayer1.message (ace_layer1.py:58-85) and its autograd backward: the exact density-projection
+ * form of the layer-1 convolution.  Forward: B[i][m][s * 64 + q] = sum over the receiver's edges whose sender has
+ * species s of ht_q(r) Y_m (S <= 4 species, S_pad >= S species blocks, pad blocks 0) and rho[i] = sum of the edge
+ * densities; the 64 -> 128-channel map, linear and skip_tp are applied by mm_linear with folded weights.
+ * Backward from gB = dL/dB: part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m (one partial, for mm_edge_grad).
+ * tab: ht(r) = h3(r) f_cut(r) per knot interval, float4 (a0..a3) [M - 1][64], built by mm_spline_coeffs_flat from
+ * mm_radial_mlp_f64 samples (D = 64 features, last layer = identity). */
+int mm_ace1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S, int S_pad,
+                float* B, float* rho, mm_stream_t stream);
+int mm_ace1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S, int S_pad,
+                const float* gB, float inv_h, float* part, mm_stream_t stream);
+int mm_spline_coeffs_flat(const double* samples, int M, int D, double eps, double h, int tab, float* coef,
+                          mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- FusedConvTP
  * Replace FusedConvTP.forward (fused_conv.py:33-37: the cuEquivariance channelwise-TP polynomial of

@@ -1,0 +1,194 @@
+// Layer-1 edge convolution in the exact "density projection" (ACE) form, on MFMA.
+//
+// In layer 1 the sender features depend only on the sender's species s and the radial weights are linear in the
+// last hidden layer of the radial MLP:  W_e[w, c] = sum_q ht_q(r_e) A3[q, w, c], with ht = h * f_cut.  So the
+// message of receiver i factors as
+//     A[i, m, c] = coef_l(m) sum_{s,q} B_i[s, q, m] A3[q, l(m), c] Xs[s, c],
+//     B_i[s, q, m] = sum_{e: recv = i, species(send) = s} ht_q(r_e) Y_m(e)                  (64 x 16 per species)
+// (the reference's ace_layer1.py:1-104 states the identity).  The per-edge work is the outer product ht x Y;
+// the 64 -> 128-channel maps (and the following linear / skip_tp) become one GEMM per atom (mm_linear).
+//
+// mm_ace1_fwd: one wave per receiver; B_i accumulated with v_mfma_f32_16x16x4f32 taking 4 edges per step:
+//   A operand (16 q x 4 edges) = ht, lane (i, g) -> q = 16 mt + i of edge g; B operand (4 edges x 16 m) = Y.
+//   Output layout B[i][m][s * 64 + q] (S_pad species blocks, pad species written as 0), rho[i] = sum of the edge
+//   densities.
+// mm_ace1_bwd: given gB = dL/dB, per edge dL/dY_m = sum_q ht_q gB[s_e, q, m] and dL/dr = sum_m Y_m
+//   sum_q ht'_q gB[s_e, q, m]: two GEMMs per tile of 16 edges (A operand = ht or ht' of edge i at q = 4 k + g,
+//   B operand = gB), then a 16-lane sum over m.  Writes part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m.
+// ht is a cubic spline per knot interval: float4 (a0..a3) coef[row][64], row = table * (M - 1) + interval.
+#include "common.h"
+
+#define MM_ACE_H 64
+#define MM_ACE_MAX_S 4
+
+template <int S>
+__global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict__ rowptr, int nC,
+                                                          const floatx4* __restrict__ e_pk,
+                                                          const float* __restrict__ e_Y,
+                                                          const floatx4* __restrict__ tab, int S_pad,
+                                                          float* __restrict__ Bout, float* __restrict__ rho) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= nC) return;
+  const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
+  const int e0 = rowptr[i], e1 = rowptr[i + 1];
+  floatx4 acc[S][4];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) acc[s][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float dsum = 0.f;
+  for (int kb = e0; kb < e1; kb += 4) {
+    const int e = kb + g;
+    const bool valid = e < e1;
+    const floatx4 pk = valid ? e_pk[e] : floatx4{0.f, 0.f, 0.f, 0.f};
+    const float y = valid ? e_Y[(size_t)e * 16 + i16] : 0.f;
+    const int se = valid ? __float_as_int(pk.z) : -1;
+    const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
+    const float t = pk.x;
+    if (i16 == 0) dsum += pk.w;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const floatx4 c = tp[16 * mt];
+      const float h = valid ? fmaf(fmaf(fmaf(c.w, t, c.z), t, c.y), t, c.x) : 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        acc[s][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? h : 0.f, y, acc[s][mt], 0, 0, 0);
+    }
+  }
+  // C layout: lane (j = i16, g) holds rows 4 g + v (q within the 16-block mt) of column m = j
+  float* __restrict__ op = Bout + (size_t)i * 16 * S_pad * MM_ACE_H + (size_t)i16 * S_pad * MM_ACE_H + 4 * g;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) *(floatx4*)(op + s * MM_ACE_H + 16 * mt) = acc[s][mt];
+  for (int s = S; s < S_pad; ++s)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) *(floatx4*)(op + s * MM_ACE_H + 16 * mt) = floatx4{0.f, 0.f, 0.f, 0.f};
+  dsum += __shfl_xor(dsum, 16);
+  dsum += __shfl_xor(dsum, 32);
+  if (lane == 0) rho[i] = dsum;
+}
+
+template <int S>
+__global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict__ rowptr, int nC,
+                                                          const floatx4* __restrict__ e_pk,
+                                                          const float* __restrict__ e_Y,
+                                                          const floatx4* __restrict__ tab, int S_pad,
+                                                          const float* __restrict__ gB, float inv_h,
+                                                          float* __restrict__ part) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= nC) return;
+  const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
+  const int e0 = rowptr[i], e1 = rowptr[i + 1];
+  // B operand of step k (4 q x 16 m): lane (j = i16, g) holds gB[i][m = j][s * 64 + 4 k + g]
+  float gb[S][16];
+  const float* __restrict__ gp = gB + (size_t)i * 16 * S_pad * MM_ACE_H + (size_t)i16 * S_pad * MM_ACE_H + g;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int k = 0; k < 16; ++k) gb[s][k] = gp[s * MM_ACE_H + 4 * k];
+  for (int tb = e0; tb < e1; tb += 16) {
+    const int e = tb + i16;          // A-operand row: edge i16 of the tile
+    const bool valid = e < e1;
+    const floatx4 pk = valid ? e_pk[e] : floatx4{0.f, 0.f, 0.f, 0.f};
+    const int se = valid ? __float_as_int(pk.z) : -1;
+    const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + g;
+    const float t = pk.x;
+    floatx4 dY = {0.f, 0.f, 0.f, 0.f}, dYp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const floatx4 c = tp[4 * k];
+      const float h = valid ? fmaf(fmaf(fmaf(c.w, t, c.z), t, c.y), t, c.x) : 0.f;
+      const float hp = valid ? fmaf(fmaf(3.f * c.w, t, 2.f * c.z), t, c.y) : 0.f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        dY = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? h : 0.f, gb[s][k], dY, 0, 0, 0);
+        dYp = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? hp : 0.f, gb[s][k], dYp, 0, 0, 0);
+      }
+    }
+    // C layout: lane (j = i16 = m, g) holds edges tb + 4 g + v of column m
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int ev = tb + 4 * g + v;
+      const bool ok = ev < e1;
+      const float y = ok ? e_Y[(size_t)ev * 16 + i16] : 0.f;
+      const float gr = mm_row_sum16(dYp[v] * y);
+      if (ok) {
+        float* __restrict__ pp = part + (size_t)ev * 17;
+        pp[1 + i16] = dY[v];
+        if (i16 == 0) pp[0] = gr * inv_h;
+      }
+    }
+  }
+}
+
+template <int S>
+static void launch_fwd(dim3 grid, hipStream_t stream, const int* rowptr, int nC, const float* e_pk, const float* e_Y,
+                       const float* tab, int S_pad, float* Bout, float* rho) {
+  hipLaunchKernelGGL(mm_ace1_fwd_kernel<S>, grid, dim3(256), 0, stream, rowptr, nC, (const floatx4*)e_pk, e_Y,
+                     (const floatx4*)tab, S_pad, Bout, rho);
+}
+
+template <int S>
+static void launch_bwd(dim3 grid, hipStream_t stream, const int* rowptr, int nC, const float* e_pk, const float* e_Y,
+                       const float* tab, int S_pad, const float* gB, float inv_h, float* part) {
+  hipLaunchKernelGGL(mm_ace1_bwd_kernel<S>, grid, dim3(256), 0, stream, rowptr, nC, (const floatx4*)e_pk, e_Y,
+                     (const floatx4*)tab, S_pad, gB, inv_h, part);
+}
+
+extern "C" int mm_ace1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S,
+                           int S_pad, float* B, float* rho, hipStream_t stream) {
+  MM_CHECK_ARG(nC >= 0 && S >= 1 && S <= MM_ACE_MAX_S && S_pad >= S, "bad sizes (1 <= S <= 4, S_pad >= S)");
+  if (nC == 0) return MM_OK;
+  const dim3 grid((nC + 3) / 4);
+  switch (S) {
+    case 1: launch_fwd<1>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
+    case 2: launch_fwd<2>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
+    case 3: launch_fwd<3>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
+    default: launch_fwd<4>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
+  }
+  return mm::launch_status("mm_ace1_fwd");
+}
+
+extern "C" int mm_ace1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S,
+                           int S_pad, const float* gB, float inv_h, float* part, hipStream_t stream) {
+  MM_CHECK_ARG(nC >= 0 && S >= 1 && S <= MM_ACE_MAX_S && S_pad >= S, "bad sizes (1 <= S <= 4, S_pad >= S)");
+  if (nC == 0) return MM_OK;
+  const dim3 grid((nC + 3) / 4);
+  switch (S) {
+    case 1: launch_bwd<1>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
+    case 2: launch_bwd<2>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
+    case 3: launch_bwd<3>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
+    default: launch_bwd<4>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
+  }
+  return mm::launch_status("mm_ace1_bwd");
+}
+
+// samples [3, M, D] (values, values at r + eps, at r - eps) -> coef[tab][k][d] float4 (a0..a3 in t), the
+// interpolant of mm_spline_coeffs in a flat layout (no channel blocks).
+__global__ void mm_spline_coeffs_flat_kernel(const double* __restrict__ samples, int M, int D, double eps, double h,
+                                             int tab, float* __restrict__ coef) {
+  const long idx = blockIdx.x * (long)blockDim.x + threadIdx.x;
+  if (idx >= (long)(M - 1) * D) return;
+  const int k = (int)(idx / D), d = (int)(idx % D);
+  const double* V = samples;
+  const double* Vp = samples + (size_t)M * D;
+  const double* Vm = samples + (size_t)2 * M * D;
+  const double v0 = V[(size_t)k * D + d], v1 = V[(size_t)(k + 1) * D + d];
+  const double g0 = (Vp[(size_t)k * D + d] - Vm[(size_t)k * D + d]) / (2 * eps) * h;
+  const double g1 = (Vp[(size_t)(k + 1) * D + d] - Vm[(size_t)(k + 1) * D + d]) / (2 * eps) * h;
+  float* p = coef + 4 * (((size_t)tab * (M - 1) + k) * D + d);
+  p[0] = (float)v0;
+  p[1] = (float)g0;
+  p[2] = (float)(-3 * v0 - 2 * g0 + 3 * v1 - g1);
+  p[3] = (float)(2 * v0 + g0 - 2 * v1 + g1);
+}
+
+extern "C" int mm_spline_coeffs_flat(const double* samples, int M, int D, double eps, double h, int tab, float* coef,
+                                     hipStream_t stream) {
+  MM_CHECK_ARG(M >= 2 && D >= 1 && tab >= 0, "bad sizes");
+  const long n = (long)(M - 1) * D;
+  hipLaunchKernelGGL(mm_spline_coeffs_flat_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, samples,
+                     M, D, eps, h, tab, coef);
+  return mm::launch_status("mm_spline_coeffs_flat");
+}

@@ -2,7 +2,8 @@
 //
 // mm_edge_geom_rij / mm_edge_geom_pos: edge vector (fp64 in, fp32 out, as the reference's rij.to(dtype),
 // mliap_threepass.py:326) stored as (unit vector, length) -- the convolutions evaluate the spherical harmonics from
-// it --, local receiver index, and one packed record per edge
+// it; e_Y (optional, for the layer-1 ACE kernels) receives the 16 harmonics --, local receiver index, and one packed
+// record per edge
 // for the convolutions: (t, spline interval row = table(pair) * (M - 1) + k, feature row of the sender, edge
 // density d = tanh((B(r) . w / sqrt(nb))^2) f_cut(r)) (fast_layers.py:154-156, 179-183, 190-192); d'(r) separately.
 // mm_edge_grad: dL/dv_e = dL/dr u + (I - u u^T) grad_u(sum_m dL/dY_m Y_m) / r, with dL/dr and dL/dY summed
@@ -60,11 +61,20 @@ __device__ __forceinline__ void mm_geom_common(int e, float vx, float vy, float 
                                                const int* __restrict__ node_spec, int S,
                                                const int* __restrict__ pair_map, const MMDensity& dp,
                                                const MMSpline& sp, int x_from_spec, float4* __restrict__ e_u,
-                                               float4* __restrict__ e_pk, int* __restrict__ e_recv,
-                                               float* __restrict__ e_dd) {
+                                               float* __restrict__ e_Y, float4* __restrict__ e_pk,
+                                               int* __restrict__ e_recv, float* __restrict__ e_dd) {
   const float r = sqrtf(vx * vx + vy * vy + vz * vz);
   const float ir = 1.0f / r;
   e_u[e] = make_float4(vx * ir, vy * ir, vz * ir, r);
+  if (e_Y) {
+    float Y[16];
+    mm_sh16(vx * ir, vy * ir, vz * ir, Y);
+    float4* __restrict__ yp = (float4*)(e_Y + (size_t)e * 16);
+    yp[0] = make_float4(Y[0], Y[1], Y[2], Y[3]);
+    yp[1] = make_float4(Y[4], Y[5], Y[6], Y[7]);
+    yp[2] = make_float4(Y[8], Y[9], Y[10], Y[11]);
+    yp[3] = make_float4(Y[12], Y[13], Y[14], Y[15]);
+  }
   const int tab = pair_map[node_spec[send] * S + node_spec[recv]];
   const float x = fminf(fmaxf((r - sp.r_lo) * sp.inv_h, 0.f), (float)(sp.M - 1) - 1e-4f);
   const float kf = floorf(x);
@@ -80,14 +90,14 @@ __device__ __forceinline__ void mm_geom_common(int e, float vx, float vy, float 
 __global__ void mm_edge_geom_rij_kernel(int E, const double* __restrict__ rij, const int* __restrict__ pair_i, int a,
                                         const int* __restrict__ ls, const int* __restrict__ node_spec, int S,
                                         const int* __restrict__ pair_map, MMDensity dp, MMSpline sp, int x_from_spec,
-                                        float4* e_u, float4* e_pk, int* e_recv, float* e_dd) {
+                                        float4* e_u, float* e_Y, float4* e_pk, int* e_recv, float* e_dd) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
   const float vx = (float)rij[3 * (size_t)e + 0];
   const float vy = (float)rij[3 * (size_t)e + 1];
   const float vz = (float)rij[3 * (size_t)e + 2];
-  mm_geom_common(e, vx, vy, vz, pair_i[e] - a, ls[e], node_spec, S, pair_map, dp, sp, x_from_spec, e_u, e_pk,
-                 e_recv, e_dd);
+  mm_geom_common(e, vx, vy, vz, pair_i[e] - a, ls[e], node_spec, S, pair_map, dp, sp, x_from_spec, e_u, e_Y,
+                 e_pk, e_recv, e_dd);
 }
 
 // x_i - x_j - L * rint((x_i - x_j) / L), every operation rounded separately (no FMA contraction), as torch's
@@ -103,7 +113,8 @@ __global__ void mm_edge_geom_pos_kernel(int E, const double* __restrict__ pos, d
                                         const int* __restrict__ recv_local, int a, const int* __restrict__ ls,
                                         const int* __restrict__ nodes, const int* __restrict__ node_spec, int S,
                                         const int* __restrict__ pair_map, MMDensity dp, MMSpline sp,
-                                        int x_from_spec, float4* e_u, float4* e_pk, int* e_recv, float* e_dd) {
+                                        int x_from_spec, float4* e_u, float* e_Y, float4* e_pk, int* e_recv,
+                                        float* e_dd) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
   const int rl = recv_local[e];
@@ -115,7 +126,7 @@ __global__ void mm_edge_geom_pos_kernel(int E, const double* __restrict__ pos, d
   for (int k = 0; k < 3; ++k) v[k] = mm_mic_f64(pos[3 * gi + k], pos[3 * gj + k], b[k]);
   (void)a;
   mm_geom_common(e, (float)v[0], (float)v[1], (float)v[2], rl, sl, node_spec, S, pair_map, dp, sp, x_from_spec,
-                 e_u, e_pk, e_recv, e_dd);
+                 e_u, e_Y, e_pk, e_recv, e_dd);
 }
 
 __global__ void mm_edge_grad_kernel(int E, const float* __restrict__ part, long part_stride, int n_part,
@@ -166,22 +177,23 @@ static int make_density(MMDensity& dp, const float* w, int nb, float r_max, int 
 extern "C" int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* ls,
                                 const int* node_spec, int S, const int* pair_map, const float* dens_w, int nb,
                                 float r_max, int p_cut, int M, float r_lo, float inv_h, int x_from_spec,
-                                float* e_u, float* e_pk, int* e_recv, float* e_dd, hipStream_t stream) {
+                                float* e_u, float* e_Y, float* e_pk, int* e_recv, float* e_dd, hipStream_t stream) {
   MM_CHECK_ARG(E >= 0 && S >= 1 && M >= 2, "bad sizes");
   MMDensity dp;
   MM_CHECK_ARG(make_density(dp, dens_w, nb, r_max, p_cut) == MM_OK, "nb out of range");
   const MMSpline sp{M, r_lo, inv_h};
   if (E == 0) return MM_OK;
   hipLaunchKernelGGL(mm_edge_geom_rij_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, E, rij, pair_i, a, ls,
-                     node_spec, S, pair_map, dp, sp, x_from_spec, (float4*)e_u, (float4*)e_pk, e_recv, e_dd);
+                     node_spec, S, pair_map, dp, sp, x_from_spec, (float4*)e_u, e_Y, (float4*)e_pk, e_recv,
+                     e_dd);
   return mm::launch_status("mm_edge_geom_rij");
 }
 
 extern "C" int mm_edge_geom_pos(int E, const double* pos, const double* box, const int* recv_local, int a,
                                 const int* ls, const int* nodes, const int* node_spec, int S, const int* pair_map,
                                 const float* dens_w, int nb, float r_max, int p_cut, int M, float r_lo,
-                                float inv_h, int x_from_spec, float* e_u, float* e_pk, int* e_recv, float* e_dd,
-                                hipStream_t stream) {
+                                float inv_h, int x_from_spec, float* e_u, float* e_Y, float* e_pk, int* e_recv,
+                                float* e_dd, hipStream_t stream) {
   MM_CHECK_ARG(E >= 0 && S >= 1 && box != nullptr && M >= 2, "bad sizes");
   MMDensity dp;
   MM_CHECK_ARG(make_density(dp, dens_w, nb, r_max, p_cut) == MM_OK, "nb out of range");
@@ -189,7 +201,7 @@ extern "C" int mm_edge_geom_pos(int E, const double* pos, const double* box, con
   if (E == 0) return MM_OK;
   hipLaunchKernelGGL(mm_edge_geom_pos_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, E, pos, box[0], box[1],
                      box[2], recv_local, a, ls, nodes, node_spec, S, pair_map, dp, sp, x_from_spec, (float4*)e_u,
-                     (float4*)e_pk, e_recv, e_dd);
+                     e_Y, (float4*)e_pk, e_recv, e_dd);
   return mm::launch_status("mm_edge_geom_pos");
 }
 

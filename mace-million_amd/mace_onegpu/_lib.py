@@ -36,8 +36,12 @@ SIGNATURES = {
     "mm_nl_filter_count": [P, L, P, P, P, D, P, P],
     "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P],
     # geometry
-    "mm_edge_geom_rij": [I, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P],
-    "mm_edge_geom_pos": [I, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P],
+    "mm_edge_geom_rij": [I, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
+    "mm_edge_geom_pos": [I, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
+    # layer-1 ACE kernels
+    "mm_ace1_fwd": [P, I, P, P, P, I, I, P, P, P],
+    "mm_ace1_bwd": [P, I, P, P, P, I, I, P, F, P, P],
+    "mm_spline_coeffs_flat": [P, I, I, D, D, I, P, P],
     "mm_edge_grad": [I, P, L, I, P, P, P, P, P, I, P],
     # convolutions (generated)
     "mm_conv1_fwd": [P, I, P, P, P, I, P, I, I, P, P, P],

@@ -27,6 +27,8 @@ from ._lib import K, stream
 C = 128
 NCB = 8
 SRC = 3                         # max K-chunks of one linear output component (mm_linear)
+ACE_H = 64                      # hidden features of the layer-1 ACE kernels (csrc/ace.hip)
+ACE_MAX_S = 4                   # species per system of the layer-1 ACE kernels
 
 
 def mfma_block(W):
@@ -73,7 +75,7 @@ class FastLayers:
     species_cols: sorted model element indices present in the system (the reference's `cols`,
     mliap_threepass.py:217); spline_grid: knots M of the radial-weight tables (reference default 512)."""
 
-    def __init__(self, model, species_cols, spline_grid=512, r_lo=0.5, device="cuda"):
+    def __init__(self, model, species_cols, spline_grid=512, r_lo=0.5, device="cuda", ace_layer1=True):
         self.dev = torch.device(device)
         sp = model.spec
         self.spec = sp
@@ -140,6 +142,11 @@ class FastLayers:
         self.n_tab = 1
         self.pair_map = torch.zeros(S * S, dtype=torch.int32, device=dev)
         self.tab = [self._build_table(P, k) for k in range(2)]
+        # -------- layer 1 in the exact density-projection (ACE) form: per-edge ht x Y outer products on MFMA,
+        # one GEMM per atom with the folded weights G[l, s_recv] (up to 4 species)
+        self.ace = bool(ace_layer1) and S <= ACE_MAX_S
+        if self.ace:
+            self._build_ace(P, comb)
         # -------- linear plans
         o1, _ = comp_of([0, 1, 2, 3])
         self.plan_l1 = LinPlan([((o1[l] + m) * C, [((o1[l] + m) * C, l)]) for l in range(4) for m in range(2 * l + 1)])
@@ -200,6 +207,54 @@ class FastLayers:
             K.mm_spline_coeffs(samples, M, nW, eps, self.h, tb, self.n_tab, coef, stream())
         return coef
 
+    def _build_ace(self, P, comb):
+        """Table of ht(r) = h3(r) f_cut(r) (the last hidden layer of layer 1's radial MLP times the cutoff) and the
+        folded weights G[l, s_recv][(s, q), c'] = coef_l sum_c A3[q, l, c] Xs[s, c] Wcomb[s_recv, l][c, c']."""
+        dev, S = self.dev, self.S
+        H = P["i0_r1"].shape[0]
+        assert H == ACE_H, "the ACE kernels are built for 64 hidden features"
+        Ws = [P[f"i0_r{j}"].to(dev).contiguous() for j in range(3)]
+        eye = (math.sqrt(H) * torch.eye(H, dtype=torch.float64, device=dev)).contiguous()
+        M = self.M
+        r = torch.linspace(self.r_lo, self.r_hi, M, dtype=torch.float64, device=dev)
+        eps = 1e-5 * (self.r_hi - self.r_lo)
+        pts = torch.cat([r, r + eps, r - eps]).contiguous()
+        samples = torch.empty(3 * M, H, dtype=torch.float64, device=dev)
+        K.mm_radial_mlp_f64(3 * M, pts, Ws[0], Ws[1], Ws[2], eye, self.spec.num_bessel, H, H, self.spec.r_max,
+                            self.spec.p_cutoff, mm.SILU_NORM, samples, stream())
+        self.tab_h = torch.empty((M - 1) * H * 4, dtype=torch.float32, device=dev)
+        K.mm_spline_coeffs_flat(samples, M, H, eps, self.h, 0, self.tab_h, stream())
+        # coupling of layer 1: node features 0e, so path w = l couples Y_m (m in l) to message component m
+        coef = {}
+        for (w, k, m, o, c) in self.tables.tp1["terms"]:
+            l = self.tables.tp1["paths"][w][2]
+            assert k == 0 and o == m and l * l <= m < (l + 1) ** 2 and self.tables.tp1["paths"][w][3] == l
+            assert abs(coef.setdefault(l, c) - c) < 1e-12
+        A3 = (P["i0_r3"] / math.sqrt(H)).view(H, 4, C)                                  # [q, l, c]
+        emb = P["emb"][self.cols] / math.sqrt(self.spec.num_elements)
+        Xs = emb @ P["i0_up"][0] / math.sqrt(C)                                          # [s, c]
+        self.S_pad = S + (S % 2)
+        nJ = self.S_pad // 2
+        self.ace_nJ = nJ
+        Gs, GTs = [], []
+        for sr in range(S):
+            for l in range(4):
+                Wc = comb[sr * 4 + l]                                                    # [c, c']
+                full = torch.zeros(self.S_pad * H, C, dtype=torch.float64)
+                for s in range(S):
+                    full[s * H:(s + 1) * H] = coef[l] * (A3[:, l, :] * Xs[s][None, :]) @ Wc
+                for j in range(nJ):
+                    blk = full[j * 128:(j + 1) * 128]
+                    Gs.append(blk)
+                    GTs.append(blk.T)
+        self.W_ace = torch.cat([mfma_block(m.to(torch.float32)) for m in Gs]).to(dev)
+        self.W_aceT = torch.cat([mfma_block(m.to(torch.float32)) for m in GTs]).to(dev)
+        Kp = self.S_pad * H
+        self.ace_Kp = Kp
+        lm = [l for l in range(4) for _ in range(2 * l + 1)]
+        self.plan_ace = LinPlan([(m * C, [(m * Kp + j * 128, lm[m] * nJ + j) for j in range(nJ)]) for m in range(16)])
+        self.plan_aceT = LinPlan([(m * Kp + j * 128, [(m * C, lm[m] * nJ + j)]) for m in range(16) for j in range(nJ)])
+
     def layer1_cache(self, n_atoms):
         """Pass-A cache of the layer-1 message and density for n_atoms receivers (8 KiB per atom)."""
         return dict(M=torch.empty(n_atoms, 16 * C, dtype=torch.float32, device=self.dev),
@@ -220,6 +275,7 @@ class FastLayers:
         i = dict(dtype=torch.int32, device=dev)
         ws = dict(nC=nC, nN=n_nodes, E=E)
         ws.update(e_u=torch.empty(E, 4, **f), e_pk=torch.empty(E, 4, **f),
+                  e_Y=torch.empty(E, 16, **f) if self.ace else None,
                   e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
         ws.update(spec=torch.empty(n_nodes, **i), lists=torch.empty(self.S * nC, **i), counts=torch.empty(self.S, **i))
         ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
@@ -248,14 +304,15 @@ class FastLayers:
         ws = self.ws
         sp = self.spec
         x_from_spec = 1 if k == 0 else 0          # layer-1 sender features depend on the species only
+        e_Y = ws["e_Y"] if (k == 0 and self.ace) else None
         if g.rij is not None:
             K.mm_edge_geom_rij(g.nE, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
                                sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo, self.inv_h, x_from_spec,
-                               ws["e_u"], ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
+                               ws["e_u"], e_Y, ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
         else:
             K.mm_edge_geom_pos(g.nE, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
                                self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo,
-                               self.inv_h, x_from_spec, ws["e_u"], ws["e_pk"], ws["e_recv"],
+                               self.inv_h, x_from_spec, ws["e_u"], e_Y, ws["e_pk"], ws["e_recv"],
                                ws["e_dd"], stream())
 
     def prepare(self, g):
@@ -271,10 +328,17 @@ class FastLayers:
         contraction input) and the density."""
         ws = self.ws
         self._geometry(0, g)
-        self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
-                    self.Xs1, C, self.tab[0], self.n_tab, self.M, ws["A"], rho_out, stream())
-        self._lin(self.plan_l1, ws["A"], 16 * C, M_out, 16 * C, self.W_l1, g.nC, scale=rho_out, scale_mode=1,
-                  species=True, w_group_stride=4)
+        if self.ace:
+            Kp = self.ace_Kp
+            self._timed("ace1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_ace1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+                        self.tab_h, self.S, self.S_pad, ws["A"], rho_out, stream())
+            self._lin(self.plan_ace, ws["A"], 16 * Kp, M_out, 16 * C, self.W_ace, g.nC, scale=rho_out, scale_mode=1,
+                      species=True, w_group_stride=4 * self.ace_nJ)
+        else:
+            self._timed("conv1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_fwd, g.rowptr, g.nC, ws["e_pk"],
+                        ws["e_u"], self.Xs1, C, self.tab[0], self.n_tab, self.M, ws["A"], rho_out, stream())
+            self._lin(self.plan_l1, ws["A"], 16 * C, M_out, 16 * C, self.W_l1, g.nC, scale=rho_out, scale_mode=1,
+                      species=True, w_group_stride=4)
         K.mm_symc1_fwd(g.nC, M_out, 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C, stream())
         self._lin(self.plan_p1, ws["B"], 4 * C, h1_out, 4 * C, self.W_p1, g.nC)
 
@@ -304,12 +368,21 @@ class FastLayers:
         self._lin(self.plan_p1, ws["gh"], D1, ws["gB"], D1, self.W_p1T, g.nC)
         K.mm_symc1_bwd(g.nC, Mc, 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1, ws["gM"], 16 * C, rho, ws["g_rho"],
                        stream())
-        self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=rho, scale_mode=1,
-                  species=True, w_group_stride=4)
-        self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
-                    self.Xs1, C, self.tab[0], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17,
-                    None, stream())
-        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
+        if self.ace:
+            Kp = self.ace_Kp
+            self._lin(self.plan_aceT, ws["gM"], 16 * C, ws["gA"], 16 * Kp, self.W_aceT, g.nC, scale=rho,
+                      scale_mode=1, species=True, w_group_stride=4 * self.ace_nJ)
+            self._timed("ace1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_ace1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+                        self.tab_h, self.S, self.S_pad, ws["gA"], self.inv_h, ws["part"], stream())
+            n_part = 1
+        else:
+            self._lin(self.plan_l1, ws["gM"], 16 * C, ws["gA"], 16 * C, self.W_l1T, g.nC, scale=rho, scale_mode=1,
+                      species=True, w_group_stride=4)
+            self._timed("conv1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv1_bwd, g.rowptr, g.nC, ws["e_pk"],
+                        ws["e_u"], self.Xs1, C, self.tab[0], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
+                        ws["E"] * 17, None, stream())
+            n_part = NCB
+        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, n_part, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
                        PF[g.e0:g.e1], 1, stream())
 
     # ------------------------------------------------------------------ layer 2

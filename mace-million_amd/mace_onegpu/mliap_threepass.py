@@ -110,7 +110,9 @@ class ThreePassMLIAP(MLIAPUnified):
             p.requires_grad_(False)
         cols = sorted(int(c) for c in torch.unique(elems).tolist())
         self._cols = cols
-        self._fl = fast_layers.FastLayers(self.model, cols, spline_grid=self.spline_grid, device=dev)
+        # MACE3P_ACE_L1=1 (default): layer 1 in the exact density-projection form (csrc/ace.hip)
+        ace = os.environ.get("MACE3P_ACE_L1", "1") == "1"
+        self._fl = fast_layers.FastLayers(self.model, cols, spline_grid=self.spline_grid, device=dev, ace_layer1=ace)
         self.scale, self.shift = self._fl.scale, self._fl.shift
         self._e0 = self._fl.e0
         self._loc = None

@@ -138,8 +138,9 @@ class ReceiverChunkMACE:
     """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
 
     def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True, use_graphs=False,
-                 e_align=65536):
+                 e_align=65536, ace_layer1=True):
         self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
+        self.ace_layer1 = bool(ace_layer1)       # layer 1 in the exact density-projection form (csrc/ace.hip)
         self.dev = torch.device(device)
         self.fl = None
         self.D1 = 4 * model.spec.C
@@ -155,7 +156,7 @@ class ReceiverChunkMACE:
         from .fast_layers import FastLayers
         cols = sorted(int(c) for c in torch.unique(sysm.spidx.long()).tolist())
         if self.fl is None or self.fl.cols != cols:
-            self.fl = FastLayers(self.model, cols, self.spline_grid, device=self.dev)
+            self.fl = FastLayers(self.model, cols, self.spline_grid, device=self.dev, ace_layer1=self.ace_layer1)
         return self.fl
 
     def graphs(self, sysm):

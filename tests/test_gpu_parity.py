@@ -286,3 +286,28 @@ def test_layer1_cache_matches_recompute(dev, model, water_gpu):
     b = ReceiverChunkMACE(model, chunk=64, device=dev, cache_layer1=False).compute(s)
     assert abs(a[0] - b[0]) < 1e-9 * s.N
     assert float((a[3] - b[3]).abs().max()) < 1e-6 * float(b[3].abs().max())
+
+
+@pytest.mark.parametrize("species", [(8, 1), (26,), (26, 28, 24), (26, 28, 24, 27)])
+def test_ace_layer1_matches_conv_path(dev, model, species):
+    """Layer 1 in the density-projection form (per-edge ht x Y on MFMA, folded atom-level GEMM) equals the
+    spline-table convolution path (same interpolant: the spline of W is the spline of ht mapped by A3) for 1 to 4
+    species."""
+    from mace_onegpu import systems
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+    _say(f"case ace species={species}")
+    if species == (8, 1):
+        pos, box, Z = systems.water_box(64, seed=3)
+    else:
+        pos, box, Z = systems.fcc_alloy(n_cells=4, a=3.6, species=species)
+    s = System(pos, box, Z - 1, 6.0, dev)
+    s.build_neighbors()
+    a = ReceiverChunkMACE(model, chunk=100, device=dev, ace_layer1=True)
+    b = ReceiverChunkMACE(model, chunk=100, device=dev, ace_layer1=False)
+    Ea, eata, Fa, PFa = a.compute(s)
+    Eb, eatb, Fb, PFb = b.compute(s)
+    assert a.fl.ace and not b.fl.ace
+    dE = abs(Ea - Eb) / s.N
+    dF = float((Fa - Fb).abs().max())
+    _say(f"  |dE|/N {dE:.2e} max|dF| {dF:.2e} (max|F| {float(Fb.abs().max()):.2e})")
+    assert dE < 1e-8 and dF < 1e-5 * float(Fb.abs().max())
