@@ -39,10 +39,13 @@ def test_generated_sources_are_current(tmp_path):
 
 
 def test_codegen_term_coverage():
-    """Every TP term appears exactly once in the generated forward kernels."""
+    """Every TP term appears exactly once per channel of a lane in the generated forward kernels (layer 2: two
+    channels per lane, accumulators acc<o>a / acc<o>b; layer 1: one)."""
     from mace_onegpu import model
     t = model.Tables(model.MaceSpec())
-    src = open(os.path.join(ROOT, "mace-million_amd", "csrc", "gen", "conv_l2.hip")).read()
-    fwd = src.split("mm_conv2_bwd_kernel")[0]
-    assert fwd.count("acc") - fwd.count("float acc") - 2 * 40 - 40 >= len(t.tp2["terms"]) - 1
-    assert len(re.findall(r"acc\d+ = fmaf\(", fwd)) == len(t.tp2["terms"])
+    gen = os.path.join(ROOT, "mace-million_amd", "csrc", "gen")
+    fwd2 = open(os.path.join(gen, "conv_l2.hip")).read().split("mm_conv2_bwd_kernel")[0]
+    for sfx in "ab":
+        assert len(re.findall(r"acc\d+" + sfx + r" = fmaf\(", fwd2)) == len(t.tp2["terms"])
+    fwd1 = open(os.path.join(gen, "conv_l1.hip")).read().split("mm_conv1_bwd_kernel")[0]
+    assert len(re.findall(r"acc\d+ = fmaf\(", fwd1)) == len(t.tp1["terms"])
