@@ -1,18 +1,26 @@
 #!/usr/bin/env python
-"""Benchmark of the MI355X three-pass MACE path: BASELINE configuration 5 on one GPU.
+"""Benchmark of the MI355X three-pass MACE path on one GPU.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--n-mol 343000] [--chunk 131072] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5|4|3|2] [--no-cpu] [--graphs]
 
-Workload (the metric's "1M-atom water"): 343,000 rigid H2O molecules (1,029,000
-atoms) at 1.0 g/cm^3, random-init MPA-0-medium architecture, fp32 kernels, velocity-Verlet MD (dt 0.5 fs, 300 K
-Maxwell-Boltzmann start, neighbour skin 2 A, rebuild when an atom moved > 1 A).  One step = one MD step
-(per-step pair filter, energy + forces by the three passes, integration, rebuilds when due).  W untimed steps,
-then K timed steps between synchronisations.  Prints ONE JSON line.
-  roofline     : the dominant edge-convolution kernel, algorithmic bytes per launch / mean launch time measured
-                 with HIP events on the launch stream during the timed steps, against 8 TB/s HBM
-  cpu_baseline : the fp64 CPU oracle (oracle/mace_ref.py, a restatement of the reference's three-pass algorithm)
-                 on a bounded sample of the same workload (one 512-molecule box of the same generator, one full
-                 energy + force evaluation), in atom-steps/s
+Prints ONE JSON line.  Default: configuration 5, the metric's "1M-atom water" -- 343,000 rigid H2O molecules
+(1,029,000 atoms) at 1.0 g/cm^3, random-init MPA-0-medium architecture, fp32 kernels, velocity-Verlet MD (dt 0.5 fs,
+300 K Maxwell-Boltzmann start, neighbour skin 2 A, rebuild when an atom moved > 1 A).  One step = one MD step
+(per-step pair filter, energy + forces by the three passes, integration, rebuilds when due).  W untimed steps after
+the initial force call, then K timed steps between synchronisations.
+  --config 3 : 98,304-atom water, one energy + force evaluation per step (ReceiverChunkMACE, chunk 16384, full chunks
+               replayed from HIP graphs), topology of the chunks rebuilt every call
+  --config 4 : 500,000-atom FCC Fe/Ni/Cr/Co alloy (a = 3.6 A, sigma 0.05 A), one energy + force evaluation per step
+  --config 2 : edge-convolution microbenchmark on one 16,384-receiver chunk of the config-3 box with synthetic edge
+               vectors (unit directions x U[0.8, 6.0] A), features and cotangents; value = achieved algorithmic GB/s of
+               the layer-2 forward kernel, every kernel listed
+Objects beside the contract fields:
+  roofline     : the dominant kernel, algorithmic bytes per launch / mean launch time measured with HIP events on the
+                 launch stream during the timed steps, against 8 TB/s HBM; traffic = measured HBM bytes per launch
+                 from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload (or null)
+  step_roofline: atom-steps/s against the fp32 MFMA ceiling of the exact model's work per atom-step
+  cpu_baseline : the fp64 CPU oracle (oracle/mace_ref.py, a restatement of the reference's three-pass algorithm) on a
+                 bounded sample of the same workload, in the metric's unit
 """
 import argparse
 import json
@@ -26,6 +34,7 @@ sys.path.insert(0, os.path.join(ROOT, "mace-million_amd"))
 HBM_PEAK_GBS = 8000.0
 VALU_F32_PEAK_TFLOPS = 78.6      # fp32 vector FMA without packed-FP32 instructions (the build disables them)
 MFMA_F32_PEAK_TFLOPS = 157.3
+C = 128
 
 
 def conv_algorithmic(name, E, nC, N, tab, Kp=128):
@@ -33,14 +42,21 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
     tables read once).  P = distinct tables (1: this model's radial weights do not depend on the species).
     ace1_*: layer 1 in the density-projection form -- per edge the 16 B record and 16 harmonics (fwd; bwd also
     writes 17 floats), the 64-feature table once, B / gB [nC, 16, Kp] once; FLOPs = the 64 x 16 outer product
-    (fwd) or its two transposed products (bwd) plus the spline evaluation."""
-    C, P, M = 128, 1, 512
+    (fwd) or its two transposed products (bwd) plus the spline evaluation.
+    tpw_*: explicit per-edge weights (FusedConvTP) -- W [E, nW, 128] and Y read once."""
+    P, M = 1, 512
     if name.startswith("ace1"):
         tab_bytes = 16 * (M - 1) * 64
         if name == "ace1_fwd":
             return 80 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp + 4 * nC, 2 * E * 64 * 16 + 6 * E * 64
         return 148 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp, 4 * E * 64 * 16 + 10 * E * 64
     nX, nW, nO, nT = tab["nX"], tab["nW"], tab["nO"], len(tab["terms"])
+    if name.startswith("tpw"):
+        if name.endswith("fwd"):
+            return (E * (8 + 64 + 4 * nW * C) + 4 * (nC + 1) + 4 * N * nX * C + 4 * nC * nO * C,
+                    2 * E * C * nT)
+        return (E * (8 + 64 + 8 * nW * C + 8 * 16) + 4 * (nC + 1) + 8 * N * nX * C + 4 * nC * nO * C,
+                2 * E * C * 3 * nT)
     gx = 1 if name == "conv2_bwd" else 0
     if name.endswith("fwd"):
         B = 16 * E + 4 * (nC + 1) + N * (4 * nX * C + 4) + 8 * P * M * nW * C + 4 * nC * nO * C
@@ -51,7 +67,7 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
     return B, F
 
 
-def kernel_sources_digest():
+def kernel_digest():
     """sha256 over the HIP sources of the library (csrc/ and csrc/gen/), to tie measurements to the kernels."""
     import hashlib
     h = hashlib.sha256()
@@ -64,7 +80,7 @@ def kernel_sources_digest():
     return h.hexdigest()
 
 
-def measured_traffic(kernel, n_mol, chunk):
+def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this
     workload (profiles/traffic_config5_water1M.json: counters scaled by a copy kernel of known size), or None
     when no pass was recorded for this workload and these kernel sources."""
@@ -73,26 +89,84 @@ def measured_traffic(kernel, n_mol, chunk):
         return None
     with open(path) as fh:
         t = json.load(fh)
-    if (t["workload"] != {"n_mol": n_mol, "chunk": chunk} or kernel not in t["kernels"]
-            or t.get("kernel_sources_sha256") != kernel_sources_digest()):
+    if (t["workload"] != workload or kernel not in t["kernels"]
+            or t.get("kernel_sources_sha256") != kernel_digest()):
         return None
     return t["kernels"][kernel]["traffic_bytes_per_launch"]
 
 
-def cpu_baseline(seed=0):
-    """fp64 CPU oracle, one full E+F of a 512-molecule box from the same generator."""
+def summarize(name, launches, ms_total, B, F, steps):
+    sec = ms_total * 1e-3
+    k = dict(launches=launches, ms_per_launch=ms_total / launches, ms_per_step=ms_total / steps,
+             GBps=B / sec / 1e9, TFLOPs=F / sec / 1e12, hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS,
+             bytes_per_launch=B / launches, flops_per_launch=F / launches)
+    if name.startswith("ace1"):          # the edge products run on MFMA
+        k["mfma_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
+    else:
+        k["valu_frac"] = F / sec / 1e12 / VALU_F32_PEAK_TFLOPS
+    return k
+
+
+def kernel_table(fl, ktimes, steps):
+    """Per-kernel launch statistics with algorithmic bytes / FLOPs (HIP-event times)."""
+    out = {}
+    for name, d in ktimes.items():
+        tab = fl.tables.tp1 if name.startswith("conv1") else fl.tables.tp2
+        Kp = getattr(fl, "ace_Kp", 128)
+        B = sum(conv_algorithmic(name, *u, tab, Kp)[0] for u in d["units"])
+        F = sum(conv_algorithmic(name, *u, tab, Kp)[1] for u in d["units"])
+        out[name] = summarize(name, d["launches"], d["ms_total"], B, F, steps)
+    return out
+
+
+def roofline_of(kernels, workload=None):
+    if not kernels:
+        return None
+    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
+    k = kernels[dom]
+    return {"kernel": f"mm_{dom}_kernel", "bound": "hbm", "achieved": round(k["GBps"], 2), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(k["hbm_frac"], 5),
+            "traffic": measured_traffic(f"mm_{dom}_kernel", workload) if workload else None,
+            "flop_rate_TFLOPs": round(k["TFLOPs"], 3),
+            **{f: round(k[f], 4) for f in ("valu_frac", "mfma_frac") if f in k},
+            "bytes_per_launch": int(k["bytes_per_launch"]), "ms_per_launch": round(k["ms_per_launch"], 4),
+            "launches": k["launches"]}
+
+
+def step_roofline(value, pairs_per_atom, tables):
+    """Work of the exact model per atom-step (the reference's three-pass algorithm: layer-1 conv forward in pass A
+    and forward + backward in pass C, layer-2 conv forward + backward in pass B, at 2 flops per FMA; node-level
+    linears 4 L1node + 3 L2node) and the fp32 MFMA ceiling it implies."""
+    t1, t2 = tables.tp1, tables.tp2
+    n1, w1, n2, w2 = len(t1["terms"]), t1["nW"], len(t2["terms"]), t2["nW"]
+    edge = pairs_per_atom * 2 * C * ((n1 + 4 * w1) * 2 + (2 * n1 + 8 * w1) + (n2 + 4 * w2) + (3 * n2 + 8 * w2))
+    l1node = 2 * C * C * (16 + 16 + 4)
+    l2node = 2 * C * C * (40 + 4 * 1.83 + 1 + 1)
+    f_atom = edge + 4 * l1node + 3 * l2node
+    ceiling = MFMA_F32_PEAK_TFLOPS * 1e12 / f_atom
+    return {"flop_per_atom_step": round(f_atom), "ceiling_atom_steps_per_s": round(ceiling), "peak_TFLOPs":
+            MFMA_F32_PEAK_TFLOPS, "frac": round(value / ceiling, 4),
+            "note": "symmetric-contraction FLOPs not counted; the evaluated algorithm does less work (layer 1 in "
+                    "the density-projection form, pass C reuses pass A's layer-1 state)"}
+
+
+def ncores():
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline_water(n_mol=512, seed=0):
+    """fp64 CPU oracle, one full E+F of a water box from the same generator."""
+    import numpy as np
     import torch
 
     sys.path.insert(0, ROOT)
-    import numpy as np
     from mace_onegpu import model as mm, o3, systems
     from oracle import mace_ref, neighbors
 
-    ncores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(ncores)
+    torch.set_num_threads(ncores())
     model = mm.MaceModel(seed=0)
     m = mace_ref.RefModel(model, o3.coupling)
-    pos, box, Z = systems.water_box(512, seed=seed)
+    pos, box, Z = systems.water_box(n_mol, seed=seed)
     s = neighbors.SystemRef(pos, box, Z - 1, 6.0)
     NN, rp, send = s.build_neighbors()
     recv = np.repeat(np.arange(s.N), NN)
@@ -100,39 +174,107 @@ def cpu_baseline(seed=0):
     t0 = time.perf_counter()
     mace_ref.three_pass(m, s.pos, box, s.spidx, recv, send, chunk=512)
     dt = time.perf_counter() - t0
-    return dict(value=s.N / dt, unit="atom-steps/s", cores=ncores, kind="port",
-                sample=f"fp64 CPU oracle (oracle/mace_ref.three_pass), one E+F of a 512-molecule water box "
-                       f"({s.N} atoms, {len(send)} pairs, chunk 512), {dt:.1f} s on {ncores} threads")
+    return dict(value=s.N / dt, unit="atom-steps/s", cores=ncores(), kind="port",
+                sample=f"fp64 CPU oracle (oracle/mace_ref.three_pass), one E+F of a {n_mol}-molecule water box "
+                       f"({s.N} atoms, {len(send)} pairs, chunk 512), {dt:.1f} s on {ncores()} threads")
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--n-mol", type=int, default=343000)
-    ap.add_argument("--chunk", type=int, default=131072)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--copy-calib-mib", type=int, default=0,
-                    help="after the timed steps, copy a buffer of this many MiB once (a plain copy kernel of known "
-                         "size that calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
-    a = ap.parse_args()
-    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU: the multi-GPU path (spatial domain "
-                                   "decomposition with RCCL halo exchange) is designed, not built; use --gpus 1"}))
-        sys.exit(2)
+def cpu_baseline_fcc(n_cells=5):
     import numpy as np
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from mace_onegpu import model as mm, o3, systems
+    from oracle import mace_ref, neighbors
+
+    torch.set_num_threads(ncores())
+    model = mm.MaceModel(seed=0)
+    m = mace_ref.RefModel(model, o3.coupling)
+    pos, box, Z = systems.fcc_alloy(n_cells=n_cells)
+    s = neighbors.SystemRef(pos, box, Z - 1, 6.0)
+    NN, rp, send = s.build_neighbors()
+    recv = np.repeat(np.arange(s.N), NN)
+    mace_ref.silu_norm()
+    t0 = time.perf_counter()
+    mace_ref.three_pass(m, s.pos, box, s.spidx, recv, send, chunk=512)
+    dt = time.perf_counter() - t0
+    return dict(value=s.N / dt, unit="atom-steps/s", cores=ncores(), kind="port",
+                sample=f"fp64 CPU oracle (oracle/mace_ref.three_pass), one E+F of a {n_cells}^3-cell FCC Fe/Ni/Cr/Co "
+                       f"box ({s.N} atoms, {len(send)} pairs), {dt:.1f} s on {ncores()} threads")
+
+
+def cpu_baseline_conv(E_full, nC_full, nN_full, E_sample=40000):
+    """fp32 torch-CPU channelwise TP (oracle.mace_ref.channelwise_tp + scatter_sum) of layer 2 on a sample of edges,
+    scaled to the config-2 chunk and expressed in its unit (algorithmic GB/s of the layer-2 forward over the chunk's
+    E_full edges)."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from mace_onegpu import o3
+    from mace_onegpu.fused_conv import ChannelwiseTP
+    from oracle import mace_ref
+
+    torch.set_num_threads(ncores())
+    d = ChannelwiseTP([0, 1])
+    g = torch.Generator().manual_seed(0)
+    n = E_sample // 90
+    X = torch.randn(n, d.nX, C, generator=g)
+    Y = torch.randn(E_sample, 16, generator=g)
+    W = torch.randn(E_sample, d.nW, C, generator=g)
+    send = torch.randint(0, n, (E_sample,), generator=g)
+    recv = torch.sort(torch.randint(0, n, (E_sample,), generator=g)).values
+    t0 = time.perf_counter()
+    mid = mace_ref.channelwise_tp(W, X, Y, send, d.table["paths"], d.table["in_ls"], o3.coupling)
+    mace_ref.scatter_sum(mid, recv, n)
+    dt = time.perf_counter() - t0
+    B, _ = conv_algorithmic("conv2_fwd", E_full, nC_full, nN_full, d.table)
+    t_full = dt * E_full / E_sample
+    return dict(value=B / t_full / 1e9, unit="GB/s", cores=ncores(), kind="port",
+                sample=f"torch-CPU fp32 channelwise TP + receiver sum of layer 2 (oracle/mace_ref.channelwise_tp, "
+                       f"explicit weights) on {E_sample} edges, {dt:.2f} s on {ncores()} threads, scaled to the "
+                       f"chunk's {E_full} edges ({t_full:.1f} s); bytes counted as for mm_conv2_fwd")
+
+
+def exit_multi_gpu():
+    print(json.dumps({"error": "this build runs on exactly one GPU: the multi-GPU path (spatial domain "
+                               "decomposition with RCCL halo exchange) is designed, not built; use --gpus 1"}))
+    sys.exit(2)
+
+
+def copy_calibration(mib):
+    import torch
+
+    from mace_onegpu._lib import K, stream
+    n = mib << 18
+    src = torch.empty(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    K.mm_fill_f32(src, n, 1.0, stream())      # writes n * 4 bytes
+    torch.mul(src, 2.0, out=dst)              # reads n * 4 bytes, writes n * 4 bytes
+    torch.cuda.synchronize()
+
+
+def base_line(a, metric, value, ms, unit, data, config, roof, kernels, cpu, higher=True):
+    return {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": a.steps,
+            "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32", "data": data, "config": config, "roofline": roof,
+            "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                        for k, v in kernels.items()},
+            "cpu_baseline": cpu}
+
+
+# ----------------------------------------------------------------------------- config 5: MD
+def run_md(a):
     import torch
 
     from mace_onegpu import model as mm, systems
     from mace_onegpu.md import MDRunner
 
-    dev = "cuda"
     t0 = time.perf_counter()
     pos, box, Z = systems.water_box(a.n_mol, seed=0)
     t_gen = time.perf_counter() - t0
     model = mm.MaceModel(seed=0)
-    md = MDRunner(model, pos, box, Z, chunk=a.chunk, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device=dev)
+    md = MDRunner(model, pos, box, Z, chunk=a.chunk, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device="cuda",
+                  use_graphs=a.graphs)
     N = md.skin_sys.N
     print(f"# generated {N} atoms (L = {box[0]:.3f} A) in {t_gen:.1f} s; chunk {a.chunk}", file=sys.stderr, flush=True)
     md.forces()                      # initial forces (set-up: builds the tables and chunk workspaces)
@@ -150,61 +292,229 @@ def main():
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
     if a.copy_calib_mib > 0:
-        from mace_onegpu._lib import K, stream
-        n = a.copy_calib_mib << 18
-        src = torch.empty(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        K.mm_fill_f32(src, n, 1.0, stream())      # writes n * 4 bytes
-        torch.mul(src, 2.0, out=dst)              # reads n * 4 bytes, writes n * 4 bytes
-        torch.cuda.synchronize()
-        del src, dst
+        copy_calibration(a.copy_calib_mib)
     n_pairs = int(md.pairs.E)
     value = N * a.steps / dt
-    # roofline of the dominant convolution kernel
-    kernels = {}
-    for name, d in ktimes.items():
-        tab = fl.tables.tp1 if name.startswith("conv1") else fl.tables.tp2
-        Kp = getattr(fl, "ace_Kp", 128)
-        B = sum(conv_algorithmic(name, *u, tab, Kp)[0] for u in d["units"])
-        F = sum(conv_algorithmic(name, *u, tab, Kp)[1] for u in d["units"])
-        sec = d["ms_total"] * 1e-3
-        kernels[name] = dict(launches=d["launches"], ms_per_launch=d["ms_total"] / d["launches"],
-                             ms_per_step=d["ms_total"] / a.steps, GBps=B / sec / 1e9, TFLOPs=F / sec / 1e12,
-                             hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS,
-                             bytes_per_launch=B / d["launches"], flops_per_launch=F / d["launches"])
-        if name.startswith("ace1"):      # the edge products run on MFMA
-            kernels[name]["mfma_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
-        else:
-            kernels[name]["valu_frac"] = F / sec / 1e12 / VALU_F32_PEAK_TFLOPS
-    dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"]) if kernels else None
-    roof = None
-    if dom:
-        k = kernels[dom]
-        roof = {"kernel": f"mm_{dom}_kernel", "bound": "hbm", "achieved": round(k["GBps"], 2), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(k["hbm_frac"], 5),
-                "traffic": measured_traffic(f"mm_{dom}_kernel", a.n_mol, a.chunk),
-                "flop_rate_TFLOPs": round(k["TFLOPs"], 3),
-                **{f: round(k[f], 4) for f in ("valu_frac", "mfma_frac") if f in k},
-                "bytes_per_launch": int(k["bytes_per_launch"]), "ms_per_launch": round(k["ms_per_launch"], 4),
-                "launches": k["launches"]}
+    kernels = kernel_table(fl, ktimes, a.steps)
+    roof = roofline_of(kernels, {"n_mol": a.n_mol, "chunk": a.chunk})
+    cpu = None if a.no_cpu else cpu_baseline_water()
+    line = base_line(a, "atom-steps/s (E+F, 1M-atom water, fp32, 1 GPU)", value, dt / a.steps * 1e3, "atom-steps/s",
+                     "synthetic (seeded water generator, random-init weights)",
+                     {"workload": "config5: 343,000-molecule water (1,029,000 atoms), random-init MPA-0-medium "
+                                  "architecture, velocity-Verlet MD dt 0.5 fs, skin 2 A",
+                      "atoms": N, "pairs": n_pairs, "chunk": a.chunk, "graphs": a.graphs,
+                      "rebuilds_timed": md.n_rebuild - rebuilds0,
+                      "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2),
+                      "box_A": round(float(box[0]), 4)}, roof, kernels, cpu)
+    line["step_roofline"] = step_roofline(value, n_pairs / N, fl.tables)
+    return line
+
+
+# ----------------------------------------------------------------------------- configs 3 and 4: E+F evaluations
+def run_ef(a):
+    import torch
+
+    from mace_onegpu import model as mm, systems
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+
+    if a.config == 3:
+        pos, box, Z = systems.water_box(32768, seed=0)
+        chunk = a.chunk or 16384
+        graphs = True if a.graphs is None else a.graphs
+        workload = ("config3: 32,768-molecule water (98,304 atoms), random-init MPA-0-medium architecture, one "
+                    f"three-pass E+F evaluation per step, chunk {chunk}" + (", HIP-graph chunks" if graphs else ""))
+        metric = "atom-steps/s (E+F, 98,304-atom water, fp32, 1 GPU)"
+    else:
+        pos, box, Z = systems.fcc_alloy(n_cells=50)
+        chunk = a.chunk or 131072
+        graphs = bool(a.graphs)
+        workload = ("config4: 500,000-atom FCC Fe/Ni/Cr/Co (a = 3.6 A, 50^3 cells, sigma 0.05 A), random-init "
+                    f"MPA-0-medium architecture, one three-pass E+F evaluation per step, chunk {chunk}"
+                    + (", HIP-graph chunks" if graphs else ""))
+        metric = "atom-steps/s (E+F, 500,000-atom FCC alloy, fp32, 1 GPU)"
+    model = mm.MaceModel(seed=0)
+    s = System(pos, box, Z - 1, 6.0, "cuda")
+    s.build_neighbors()
+    ev = ReceiverChunkMACE(model, chunk=chunk, device="cuda", use_graphs=graphs)
+    ev.compute(s)
+    for _ in range(a.warmup):
+        ev.compute(s)
+    fl = ev.fl
+    fl.start_kernel_timing()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        E, eat, F, PF = ev.compute(s)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ktimes = fl.stop_kernel_timing()
+    value = s.N * a.steps / dt
+    kernels = kernel_table(fl, ktimes, a.steps) if not graphs else {}
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline()
-    line = {
-        "metric": "atom-steps/s (E+F, 1M-atom water, fp32, 1 GPU)",
-        "value": round(value, 1), "unit": "atom-steps/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
-        "ms_per_step": round(dt / a.steps * 1e3, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "fp32", "data": "synthetic (seeded water generator, random-init weights)",
-        "config": {"workload": "config5: 343,000-molecule water (1,029,000 atoms), random-init MPA-0-medium "
-                               "architecture, velocity-Verlet MD dt 0.5 fs, skin 2 A",
-                   "atoms": N, "pairs": n_pairs, "chunk": a.chunk, "rebuilds_timed": md.n_rebuild - rebuilds0,
-                   "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2),
-                   "box_A": round(float(box[0]), 4)},
-        "roofline": roof,
-        "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                    for k, v in kernels.items()},
-        "cpu_baseline": cpu,
+        cpu = cpu_baseline_water() if a.config == 3 else cpu_baseline_fcc()
+    n_pairs = int(s.rowptr[-1])
+    line = base_line(a, metric, value, dt / a.steps * 1e3, "atom-steps/s",
+                     "synthetic (seeded generator, random-init weights)",
+                     {"workload": workload, "atoms": s.N, "pairs": n_pairs, "chunk": chunk, "graphs": graphs,
+                      "E_per_atom_eV": round(E / s.N, 8),
+                      "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2)},
+                     roofline_of(kernels), kernels, cpu)
+    if graphs:
+        line["roofline_note"] = "per-kernel HIP-event timing is not available inside graph replays (rocprofv3)"
+    line["step_roofline"] = step_roofline(value, n_pairs / s.N, fl.tables)
+    return line
+
+
+# ----------------------------------------------------------------------------- config 2: edge-convolution kernels
+def run_conv(a):
+    import torch
+
+    from mace_onegpu import model as mm, o3, systems
+    from mace_onegpu._lib import K, stream
+    from mace_onegpu.fused_conv import ChannelwiseTP, FusedConvTP
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+
+    pos, box, Z = systems.water_box(32768, seed=0)
+    s = System(pos, box, Z - 1, 6.0, "cuda")
+    s.build_neighbors()
+    ev = ReceiverChunkMACE(mm.MaceModel(seed=0), chunk=16384, device="cuda")
+    g = ev.graphs(s)[0]
+    fl = ev._layers(s)
+    ws = fl.prepare(g)
+    E, nC, nN = g.nE, g.nC, g.n_nodes
+    gen = torch.Generator().manual_seed(1)
+    u = torch.randn(E, 3, generator=gen, dtype=torch.float64)
+    u /= u.norm(dim=1, keepdim=True)
+    r = 0.8 + 5.2 * torch.rand(E, 1, generator=gen, dtype=torch.float64)
+    g.rij = (u * r).float().double().cuda()
+    g.pair_i = (g.recv_local + g.a).to(torch.int32)
+    gen2 = torch.Generator(device="cuda").manual_seed(2)
+    X2 = torch.randn(nN, 4 * C, device="cuda", generator=gen2)
+    gA2 = torch.randn(nC, 40 * C, device="cuda", generator=gen2)
+    Kp = getattr(fl, "ace_Kp", C)
+    gM1 = torch.randn(nC, 16 * Kp, device="cuda", generator=gen2)
+    gA1 = torch.randn(nC, 16 * C, device="cuda", generator=gen2)
+    fl._geometry(0, g)
+    pk1, eu1 = ws["e_pk"][:E].clone(), ws["e_u"][:E].clone()
+    eY1 = ws["e_Y"][:E].clone() if fl.ace else None
+    fl._geometry(1, g)
+    pk2, eu2 = ws["e_pk"][:E].clone(), ws["e_u"][:E].clone()
+    out1 = torch.empty(nC, 16 * C, device="cuda")
+    out2 = torch.empty(nC, 40 * C, device="cuda")
+    Bace = torch.empty(nC, 16 * Kp, device="cuda")
+    rho = torch.empty(nC, device="cuda")
+    part = torch.empty(8 * E * 17, device="cuda")
+    gX = torch.zeros(nN, 4 * C, device="cuda")
+    st = stream()
+    calls = {
+        "conv1_fwd": (lambda: K.mm_conv1_fwd(g.rowptr, nC, pk1, eu1, fl.Xs1, C, fl.tab[0], fl.n_tab, fl.M, out1, rho,
+                                             st), fl.tables.tp1),
+        "conv1_bwd": (lambda: K.mm_conv1_bwd(g.rowptr, nC, pk1, eu1, fl.Xs1, C, fl.tab[0], fl.n_tab, fl.M, fl.inv_h,
+                                             gA1, part, E * 17, None, st), fl.tables.tp1),
+        "conv2_fwd": (lambda: K.mm_conv2_fwd(g.rowptr, nC, pk2, eu2, X2, 4 * C, fl.tab[1], fl.n_tab, fl.M, out2, rho,
+                                             st), fl.tables.tp2),
+        "conv2_bwd": (lambda: K.mm_conv2_bwd(g.rowptr, nC, pk2, eu2, X2, 4 * C, fl.tab[1], fl.n_tab, fl.M, fl.inv_h,
+                                             gA2, part, E * 17, gX, st), fl.tables.tp2),
     }
+    if fl.ace:
+        calls["ace1_fwd"] = (lambda: K.mm_ace1_fwd(g.rowptr, nC, pk1, eY1, fl.tab_h, fl.S, fl.S_pad, Bace, rho, st),
+                             fl.tables.tp1)
+        calls["ace1_bwd"] = (lambda: K.mm_ace1_bwd(g.rowptr, nC, pk1, eY1, fl.tab_h, fl.S, fl.S_pad, gM1, fl.inv_h,
+                                                   part, st), fl.tables.tp1)
+    # explicit-weight FusedConvTP kernels (V1, V2 and the literal V3 table 0e+1o+2e+3o) on the same edges
+    Y16 = torch.from_numpy(o3.spherical_harmonics(g.rij.cpu().numpy())).float().cuda()
+    send = g.ls
+    rp = torch.zeros(nN + 1, dtype=torch.int32, device="cuda")
+    rp[: nC + 1] = g.rowptr
+    rp[nC + 1:] = g.rowptr[-1]
+    for key, ls in (("tpw_l1", [0]), ("tpw_l2", [0, 1]), ("tpw_l0123", [0, 1, 2, 3])):
+        d = ChannelwiseTP(ls)
+        Xd = torch.randn(nN, d.nX * C, device="cuda", generator=gen2)
+        Wd = torch.randn(E, d.nW * C, device="cuda", generator=gen2)
+        Od = torch.empty(nN, d.nO * C, device="cuda")
+        Gd = torch.randn(nN, d.nO * C, device="cuda", generator=gen2)
+        gWd = torch.empty_like(Wd)
+        gYp = torch.empty(8, E, 16, device="cuda")
+        gXd = torch.zeros_like(Xd)
+        f = getattr(K, f"mm_{key}_fwd")
+        b = getattr(K, f"mm_{key}_bwd")
+        calls[key + "_fwd"] = ((lambda f=f, Xd=Xd, Wd=Wd, Od=Od:
+                                f(rp, nC, None, send, Y16, 16, Wd, Wd.stride(0), Xd, Xd.stride(0), Od, Od.stride(0),
+                                  st)), d.table)
+        calls[key + "_bwd"] = ((lambda b=b, Xd=Xd, Wd=Wd, Gd=Gd, gWd=gWd, gYp=gYp, gXd=gXd:
+                                b(rp, nC, None, send, Y16, 16, Wd, Wd.stride(0), Xd, Xd.stride(0), Gd, Gd.stride(0),
+                                  gWd, gWd.stride(0), gYp, E * 16, gXd, gXd.stride(0), st)), d.table)
+    kernels = {}
+    for name, (fn, tab) in calls.items():
+        for _ in range(max(a.warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(a.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1)
+        B, F = conv_algorithmic(name, E, nC, nN, tab, Kp)
+        kernels[name] = summarize(name, a.steps, ms, B * a.steps, F * a.steps, a.steps)
+    # check the layer-2 forward against FusedConvTP fed with the spline weights of the same edges (first 256
+    # receivers): W[e, w, c] evaluated in fp64 from the kernel's interval coefficients
+    calls["conv2_fwd"][0]()
+    torch.cuda.synchronize()
+    nr = 256
+    ne = int(g.rowptr[nr])
+    coef = fl.tab[1].view(8, fl.n_tab, fl.M - 1, 10, 16, 4).double()
+    pk = pk2[:ne]
+    row = pk[:, 1].contiguous().view(torch.int32).long()
+    t = pk[:, 0].double()[None, :, None, None]
+    cw = coef[:, 0, row]                                            # [8, ne, 10, 16, 4]
+    Wsp = ((cw[..., 3] * t + cw[..., 2]) * t + cw[..., 1]) * t + cw[..., 0]
+    Wsp = Wsp.permute(1, 2, 0, 3).reshape(ne, 10 * C).float().contiguous()
+    Yc = torch.from_numpy(o3.spherical_harmonics(eu2[:ne, :3].double().cpu().numpy())).float().cuda()
+    tp = FusedConvTP(ChannelwiseTP([0, 1]), 10 * C)
+    ei = torch.stack([pk[:, 2].contiguous().view(torch.int32).long(), g.recv_local[:ne].long()])
+    ref = tp(X2, Yc, Wsp, ei)[:nr]
+    err = float((ref - out2[:nr]).abs().max() / ref.abs().max())
+    v = kernels["conv2_fwd"]
+    cpu = None if a.no_cpu else cpu_baseline_conv(E, nC, nN)
+    line = base_line(a, "edge-conv achieved algorithmic GB/s (layer-2 forward, one 16,384-receiver chunk)", v["GBps"],
+                     v["ms_per_launch"], "GB/s",
+                     "synthetic (config-3 topology; random unit directions x U[0.8, 6] A, N(0,1) features and "
+                     "cotangents, spline tables of the random-init model)",
+                     {"workload": "config2: edge-convolution kernels on chunk 0 (16,384 receivers) of the 98,304-atom "
+                                  "water box", "edges": E, "receivers": nC, "nodes": nN,
+                      "check_vs_FusedConvTP_max_rel": err}, roofline_of(kernels), kernels, cpu)
+    line["steps_note"] = "steps = launches of each kernel"
+    return line
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=5, choices=[2, 3, 4, 5])
+    ap.add_argument("--n-mol", type=int, default=343000, help="config 5: water molecules")
+    ap.add_argument("--chunk", type=int, default=None, help="receiver chunk (default: 131072; config 3: 16384)")
+    ap.add_argument("--graphs", action="store_true", default=None,
+                    help="replay full chunks from HIP graphs (default on for config 3 only)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="after the timed steps, run a plain elementwise kernel over this many MiB (reads and "
+                         "writes a buffer of known size: calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        exit_multi_gpu()
+    if a.config == 5:
+        a.chunk = a.chunk or 131072
+        a.graphs = bool(a.graphs)
+        line = run_md(a)
+    elif a.config in (3, 4):
+        line = run_ef(a)
+    else:
+        line = run_conv(a)
     print(json.dumps(line), flush=True)
 
 
