@@ -66,6 +66,8 @@ class ChunkGraphExec:
         self.eat = torch.zeros(nC, **f64)
         self.H1x = torch.zeros(nt_cap + 1, D1, **f32)      # row nt_cap: sink of the pad nodes (stays 0)
         self.G1 = torch.zeros(nt_cap + 1, D1, **f32)
+        self.lists = torch.zeros(fl.S * nC, **i32)
+        self.list_counts = torch.zeros(fl.S, **i32)
         self.ws = None
         self.graphs = None
         self.n_replays = 0
@@ -76,6 +78,7 @@ class ChunkGraphExec:
         g.a, g.b, g.e0, g.e1 = 0, self.C, 0, self.e_cap
         g.nC, g.nE, g.n_nodes = self.C, self.e_cap, self.n_cap
         g.rowptr, g.ls, g.nodes, g.node_spec = self.rowptr, self.ls, self.nodes, self.node_spec
+        g.lists, g.list_counts, g.recompute_lists = self.lists, self.list_counts, True
         if self.mode == "rij":
             g.rij, g.pair_i = self.rij, self.pair_i
         else:

@@ -277,7 +277,6 @@ class FastLayers:
         ws.update(e_u=torch.empty(E, 4, **f), e_pk=torch.empty(E, 4, **f),
                   e_Y=torch.empty(E, 16, **f) if self.ace else None,
                   e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
-        ws.update(spec=torch.empty(n_nodes, **i), lists=torch.empty(self.S * nC, **i), counts=torch.empty(self.S, **i))
         ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
                   rho=torch.empty(nC, **f), g_rho=torch.empty(nC, **f),
                   M=torch.empty(nC * 16 * C, **f), gM=torch.empty(nC * 16 * C, **f),
@@ -293,7 +292,7 @@ class FastLayers:
         ws = self.ws
         if species:
             K.mm_linear(inp, in_stride, in_rows, out, out_stride, out_rows, W, scale, scale_mode, ws["lists"],
-                        ws["counts"], ws["nC"], self.S, w_group_stride, rows, accumulate, plan.n, plan.nsrc,
+                        ws["counts"], ws["lists_stride"], self.S, w_group_stride, rows, accumulate, plan.n, plan.nsrc,
                         plan.inoff, plan.widx, plan.outoff, stream())
         else:
             K.mm_linear(inp, in_stride, in_rows, out, out_stride, out_rows, W, scale, scale_mode, None, None, 0, 1, 0,
@@ -318,8 +317,16 @@ class FastLayers:
     def prepare(self, g):
         """Per-chunk node species and per-species receiver lists (g.node_spec: compact species of local nodes)."""
         ws = self.workspace(g.nC, g.n_nodes, g.nE)
-        ws["spec"][: g.n_nodes].copy_(g.node_spec)
-        K.mm_species_lists(ws["spec"], g.nC, self.S, ws["lists"], ws["nC"], ws["counts"], stream())
+        ws["spec"] = g.node_spec
+        # per-species receiver lists of the chunk: built once per chunk object and shared by the three passes
+        # (a chunk marked recompute_lists -- the static chunk of the HIP-graph executor -- rebuilds them in place)
+        if getattr(g, "lists", None) is None:
+            g.lists = torch.empty(self.S * g.nC, dtype=torch.int32, device=self.dev)
+            g.list_counts = torch.empty(self.S, dtype=torch.int32, device=self.dev)
+            K.mm_species_lists(g.node_spec, g.nC, self.S, g.lists, g.nC, g.list_counts, stream())
+        elif getattr(g, "recompute_lists", False):
+            K.mm_species_lists(g.node_spec, g.nC, self.S, g.lists, g.nC, g.list_counts, stream())
+        ws["lists"], ws["counts"], ws["lists_stride"] = g.lists, g.list_counts, g.nC
         return ws
 
     # ------------------------------------------------------------------ layer 1
