@@ -311,3 +311,39 @@ def test_ace_layer1_matches_conv_path(dev, model, species):
     dF = float((Fa - Fb).abs().max())
     _say(f"  |dE|/N {dE:.2e} max|dF| {dF:.2e} (max|F| {float(Fb.abs().max()):.2e})")
     assert dE < 1e-8 and dF < 1e-5 * float(Fb.abs().max())
+
+
+def test_isolated_atoms_and_tiny_chunks(dev, model, ref_model):
+    """Receivers without any neighbour (empty CSR rows) and chunks of one receiver: energies and forces still match
+    the oracle (isolated atoms carry E0 + the readout of their empty-neighbourhood features and zero force)."""
+    from mace_onegpu import systems
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+    pos, box0, Z = systems.water_box(8, seed=5)               # 24 atoms in a 6.2 A cell ...
+    box = np.array([16.0, 15.0, 17.0])                         # ... placed in a larger box with empty space
+    far = np.array([[12.0, 11.0, 13.0], [13.5, 3.0, 8.0], [2.0, 12.5, 14.0]])
+    pos = np.concatenate([pos, far])
+    Z = np.concatenate([Z, [1, 8, 1]])
+    s = System(pos, box, Z - 1, 6.0, dev)
+    s.build_neighbors()
+    assert int((s.NN == 0).sum()) >= 3
+    ref = _oracle_three_pass(ref_model, s, 64)
+    for chunk in (1, 7, 64):
+        _say(f"case isolated atoms chunk={chunk}")
+        E, eat, F, PF = ReceiverChunkMACE(model, chunk=chunk, device=dev).compute(s)
+        _check(E, eat, F, ref, s.N)
+        iso = (s.NN == 0).cpu()
+        assert float(F.cpu()[iso].abs().max()) == 0.0
+
+
+def test_fmax_guard_raises(dev, model, water_gpu, monkeypatch):
+    """The non-finite / absurd-force guard (mliap_threepass.py:595-601) raises instead of handing LAMMPS the forces;
+    forced from the host with a tiny MACE3P_FMAX_ABORT (every kernel still runs normally)."""
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    monkeypatch.setenv("MACE3P_FMAX_ABORT", "1e-12")
+    s = water_gpu
+    data = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True)
+    tp = ThreePassMLIAP(model, chunk=96)
+    with pytest.raises(RuntimeError, match="absurd"):
+        tp.compute_forces(data)
+    assert data.pair_forces is None
