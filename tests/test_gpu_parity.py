@@ -320,12 +320,12 @@ def test_isolated_atoms_and_tiny_chunks(dev, model, ref_model):
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
     pos, box0, Z = systems.water_box(8, seed=5)               # 24 atoms in a 6.2 A cell ...
     box = np.array([16.0, 15.0, 17.0])                         # ... placed in a larger box with empty space
-    far = np.array([[12.0, 11.0, 13.0], [13.5, 3.0, 8.0], [2.0, 12.5, 14.0]])
+    far = np.array([[11.0, 10.6, 11.6]])                      # >= 8.4 A from every image of the cluster
     pos = np.concatenate([pos, far])
-    Z = np.concatenate([Z, [1, 8, 1]])
+    Z = np.concatenate([Z, [8]])
     s = System(pos, box, Z - 1, 6.0, dev)
     s.build_neighbors()
-    assert int((s.NN == 0).sum()) >= 3
+    assert int((s.NN == 0).sum()) == 1
     ref = _oracle_three_pass(ref_model, s, 64)
     for chunk in (1, 7, 64):
         _say(f"case isolated atoms chunk={chunk}")
