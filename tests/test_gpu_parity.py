@@ -316,11 +316,13 @@ def test_ace_layer1_matches_conv_path(dev, model, species):
 def test_isolated_atoms_and_tiny_chunks(dev, model, ref_model):
     """Receivers without any neighbour (empty CSR rows) and chunks of one receiver: energies and forces still match
     the oracle (isolated atoms carry E0 + the readout of their empty-neighbourhood features and zero force)."""
-    from mace_onegpu import systems
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
-    pos, box0, Z = systems.water_box(8, seed=5)               # 24 atoms in a 6.2 A cell ...
-    box = np.array([16.0, 15.0, 17.0])                         # ... placed in a larger box with empty space
-    far = np.array([[11.0, 10.6, 11.6]])                      # >= 8.4 A from every image of the cluster
+    O = np.array([[2.0, 2.0, 2.0], [4.5, 2.2, 2.5], [3.0, 4.5, 3.0], [2.5, 3.0, 5.0]])   # 4 molecules
+    H = np.array([[0.757, 0.586, 0.0], [-0.757, 0.586, 0.0]])
+    pos = np.concatenate([np.stack([o, o + H[0], o + H[1]]) for o in O])
+    Z = np.tile([8, 1, 1], len(O))
+    box = np.array([16.0, 15.0, 17.0])
+    far = np.array([[11.0, 10.6, 11.6]])                      # ~10 A from every image of the cluster
     pos = np.concatenate([pos, far])
     Z = np.concatenate([Z, [8]])
     s = System(pos, box, Z - 1, 6.0, dev)
