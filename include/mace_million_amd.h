@@ -53,7 +53,9 @@ int mm_nl_fill(const double* pos_sorted, const int* cell_sorted, long N, const d
 int mm_nl_filter_count(const double* pos, long N, const double* box /* HOST [3] */, const long* skin_rowptr,
                        const int* skin_send, double r_max2, int* NN, mm_stream_t stream);
 int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] */, const long* skin_rowptr,
-                      const int* skin_send, double r_max2, const long* rowptr, int* send, mm_stream_t stream);
+                      const int* skin_send, double r_max2, const long* rowptr, int* send,
+                      int* filtered_index /* nullable: per skin pair, its index in the filtered list or -1 */,
+                      mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- edge geometry
  * Replace receiver_chunk_mace.edge_embed (:230-234), the table coordinates of spline_w._coords (spline_w.py:18-27)
@@ -174,6 +176,11 @@ int mm_ghost_reverse(const float* src, float* dst, int D, int nlocal, const int*
 /* per-atom forces from pair forces (ReceiverChunkMACE._accum_forces, receiver_chunk_mace.py:272-276) */
 int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* send_rowptr, const long* send_perm,
                             const float* pair_force, double* F, mm_stream_t stream);
+/* the same per-atom forces for an MD step whose pair list was filtered from a skin list: through the skin list's
+ * reverse-pair map (rev) and the filter's index map, without sorting the pairs by sender (no counterpart in the
+ * reference, whose MD runs inside LAMMPS) */
+int mm_pair_forces_skin(long n, const long* skin_rowptr, const int* filtered_index, const int* rev,
+                        const float* pair_force, double* F, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- tables
  * conv_spline.build_tables + spline_radial._sample (conv_spline.py:230-249, spline_radial.py:116-151): the radial

@@ -232,3 +232,46 @@ extern "C" int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* s_
                      s_rowptr, s_perm, pf, F);
   return mm::launch_status("mm_pair_forces_to_atoms");
 }
+
+// Per-atom forces of an MD step from the pair forces of the filtered list, through the skin list (no sort): for
+// every skin pair e of atom i that survived the filter (fidx[e] = its index in the filtered list, -1 otherwise),
+// F[i] += -PF[fidx[e]] + PF[fidx[rev[e]]], rev[e] = the skin index of the reverse pair (j, i); the neighbour test
+// is symmetric, so the reverse pair survives with it.  One wave per atom, fp64 accumulation.
+__global__ void __launch_bounds__(256) mm_pair_forces_skin_kernel(long n, const long* __restrict__ skin_rowptr,
+                                                                  const int* __restrict__ fidx,
+                                                                  const int* __restrict__ rev,
+                                                                  const float* __restrict__ pf,
+                                                                  double* __restrict__ F) {
+  const long i = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (i >= n) return;
+  const int lane = threadIdx.x & 63;
+  double fx = 0, fy = 0, fz = 0;
+  for (long e = skin_rowptr[i] + lane; e < skin_rowptr[i + 1]; e += 64) {
+    const int f = fidx[e];
+    if (f >= 0) {
+      const long r = fidx[rev[e]];
+      fx += (double)pf[3 * r] - (double)pf[3 * (long)f];
+      fy += (double)pf[3 * r + 1] - (double)pf[3 * (long)f + 1];
+      fz += (double)pf[3 * r + 2] - (double)pf[3 * (long)f + 2];
+    }
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    fx += __shfl_xor(fx, o);
+    fy += __shfl_xor(fy, o);
+    fz += __shfl_xor(fz, o);
+  }
+  if (lane == 0) {
+    F[3 * i] = fx;
+    F[3 * i + 1] = fy;
+    F[3 * i + 2] = fz;
+  }
+}
+
+extern "C" int mm_pair_forces_skin(long n, const long* skin_rowptr, const int* fidx, const int* rev, const float* pf,
+                                   double* F, hipStream_t stream) {
+  MM_CHECK_ARG(n >= 0, "bad sizes");
+  if (n == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_pair_forces_skin_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, stream, n, skin_rowptr,
+                     fidx, rev, pf, F);
+  return mm::launch_status("mm_pair_forces_skin");
+}

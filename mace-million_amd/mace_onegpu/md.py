@@ -32,6 +32,11 @@ class PairList:
         self.NN = torch.empty(self.N, dtype=torch.int32, device=self.device)
         self.rowptr = torch.empty(self.N + 1, dtype=torch.int64, device=self.device)
         self.send = None
+        # per skin pair: its index in the filtered list (-1 if dropped) and the skin index of its reverse pair; the
+        # per-atom forces of every step are summed through them (mm_pair_forces_skin, no per-step sort)
+        E_s = int(skin_sys.rowptr[-1])
+        self.fidx = torch.empty(max(E_s, 1), dtype=torch.int32, device=self.device)
+        self.rev = reverse_pairs(skin_sys)
 
     def refresh(self):
         s = self._skin
@@ -41,10 +46,34 @@ class PairList:
         E = int(self.rowptr[-1])
         if self.send is None or self.send.numel() < E:
             self.send = torch.empty(int(E * 1.1) + 1, dtype=torch.int32, device=self.device)
-        K.mm_nl_filter_fill(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.rowptr, self.send, stream())
+        K.mm_nl_filter_fill(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.rowptr, self.send, self.fidx,
+                            stream())
         self.E = E
         self.send_view = self.send[:E]
         return E
+
+    def atom_forces(self, PF):
+        """F_i = -sum_{pairs (i, j)} PF + sum_{pairs (j, i)} PF of the current filtered list (fp64)."""
+        F = torch.empty(self.N, 3, dtype=torch.float64, device=self.device)
+        K.mm_pair_forces_skin(self.N, self._skin.rowptr, self.fidx, self.rev, PF, F, stream())
+        return F
+
+
+def reverse_pairs(sysm):
+    """rev[e] = index of the pair (j, i) for every pair e = (i, j) of a symmetric CSR neighbour list (the cell-list
+    test is symmetric bit for bit: d(j, i) = -d(i, j) exactly in fp64)."""
+    N = sysm.N
+    dev = sysm.send.device
+    recv = torch.repeat_interleave(torch.arange(N, device=dev, dtype=torch.int64), sysm.NN.long())
+    send = sysm.send.long()
+    key = recv * N + send
+    order = torch.argsort(key)
+    skey = key[order]
+    rkey = send * N + recv
+    pos = torch.searchsorted(skey, rkey).clamp_(max=max(skey.numel() - 1, 0))
+    if skey.numel() and not bool((skey[pos] == rkey).all()):
+        raise RuntimeError("neighbour list is not symmetric")
+    return order[pos].to(torch.int32)
 
 
 class MDRunner:
@@ -118,3 +147,4 @@ class _PairView:
     def __init__(self, pl):
         self.N, self.device, self.box, self.pos, self.spidx = pl.N, pl.device, pl.box, pl.pos, pl.spidx
         self.NN, self.rowptr, self.send = pl.NN, pl.rowptr, pl.send_view
+        self.atom_forces_fn = pl.atom_forces

@@ -264,6 +264,8 @@ class ReceiverChunkMACE:
 
 def pair_to_atom_forces(sysm, PF):
     """F_i = -sum_{e: recv=i} PF_e + sum_{e: send=i} PF_e (v_e = x_recv - x_send), deterministic CSR sums."""
+    if getattr(sysm, "atom_forces_fn", None) is not None:     # MD pair list filtered from a skin list
+        return sysm.atom_forces_fn(PF)
     dev, N = sysm.device, sysm.N
     if not hasattr(sysm, "_s_perm") or sysm._s_perm_E != sysm.send.numel():
         s_perm = torch.argsort(sysm.send.long(), stable=True)

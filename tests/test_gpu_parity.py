@@ -349,3 +349,22 @@ def test_fmax_guard_raises(dev, model, water_gpu, monkeypatch):
     with pytest.raises(RuntimeError, match="absurd"):
         tp.compute_forces(data)
     assert data.pair_forces is None
+
+
+def test_md_skin_forces_match_sorted_sum(dev, model):
+    """Per-atom forces of an MD step summed through the skin list's reverse-pair map (mm_pair_forces_skin) equal
+    the receiver + sender-sorted sums of mm_pair_forces_to_atoms for the same pair forces."""
+    from mace_onegpu import systems
+    from mace_onegpu.md import MDRunner, _PairView
+    from mace_onegpu.receiver_chunk_mace import pair_to_atom_forces
+    pos, box, Z = systems.water_box(512, seed=2)
+    md = MDRunner(model, pos, box, Z, chunk=1024, device=dev)
+    md.step()
+    md.step()
+    view = _PairView(md.pairs)
+    E, eat, F_skin, PF = md.ev.compute(view)
+    view.atom_forces_fn = None
+    F_sorted = pair_to_atom_forces(view, PF)
+    d = float((F_skin - F_sorted).abs().max())
+    _say(f"  skin vs sorted force sums: max|d| {d:.2e}")
+    assert d <= 1e-12 * float(F_sorted.abs().max())

@@ -82,3 +82,23 @@ def test_topology_matches_reference(ci):
         ls_all.append(ls)
     assert np.array_equal(np.concatenate(nodes_all), T[f"c{ci}__nodes"])
     assert np.array_equal(np.concatenate(ls_all), T[f"c{ci}__ls"])
+
+
+def test_reverse_pairs_map():
+    """reverse_pairs (the MD force sum's reverse-pair map) is an involution mapping (i, j) to (j, i)."""
+    import torch
+    from mace_onegpu.md import reverse_pairs
+
+    g = golden("water648_cells")
+    s = neighbors.SystemRef(g["pos"], g["box"], g["spidx"], 6.0)
+    NN, rp, send = s.build_neighbors()
+
+    class V:
+        pass
+    v = V()
+    v.N, v.NN, v.send = s.N, torch.as_tensor(NN), torch.as_tensor(send)
+    rev = reverse_pairs(v).long()
+    recv = torch.repeat_interleave(torch.arange(s.N), v.NN.long())
+    e = torch.arange(len(send))
+    assert torch.equal(rev[rev], e)
+    assert torch.equal(recv[rev], v.send.long()) and torch.equal(v.send.long()[rev], recv)
