@@ -9,9 +9,10 @@
 // Launch: grid (ceil(rows / (64 MT)), n_comp, n_groups); 256 threads = 4 waves, each wave 16 MT rows x 128
 // columns (8 MT MFMA tiles; MT = 2 for large launches); the 128x128 weight block is staged in LDS (64 KiB) in the
 // lane order of the B operand.
-// Weight blocks are stored pre-permuted: element W[k][n], k = 16 t + 4 g + u, at float index
-// ((t * 128 + n) * 4 + g) * 4 + u, so that lane (n, g) reads its 4 k-values of step t as one 16-byte LDS read and
-// the A operand of lane (row, g) is the float4 in[row][16 t + 4 g .. + 3].
+// Weight blocks are stored pre-permuted: element W[k][n], k = 16 t + 4 g + u, n = 16 nt + i, at float index
+// (((t * 8 + nt) * 4 + g) * 16 + i) * 4 + u, so that lane (i, g) reads its 4 k-values of step t and tile nt as one
+// 16-byte LDS read, the 16 lanes of a group reading 256 consecutive bytes (no bank conflicts), and the A operand of
+// lane (row, g) is the float4 in[row][16 t + 4 g .. + 3].
 #include "common.h"
 
 #define MM_LIN_MAX_COMP 48
@@ -89,7 +90,7 @@ __global__ void __launch_bounds__(256) mm_linear_kernel(MMLinArgs args) {
     for (int t = 0; t < 8; ++t) {
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const floatx4 b = Wl[(t * 128 + 16 * nt + i) * 4 + g];
+        const floatx4 b = Wl[((t * 8 + nt) * 4 + g) * 16 + i];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].x, b.x, acc[mt][nt], 0, 0, 0);

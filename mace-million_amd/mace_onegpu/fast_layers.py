@@ -32,9 +32,11 @@ ACE_MAX_S = 4                   # species per system of the layer-1 ACE kernels
 
 
 def mfma_block(W):
-    """[128, 128] (k, n) -> flat float32 in the B-operand lane order of mm_linear: index ((t*128+n)*4+g)*4+u."""
-    W = W.reshape(8, 4, 4, 128)               # [t, g, u, n]
-    return W.permute(0, 3, 1, 2).reshape(-1).contiguous()
+    """[128, 128] (k, n) -> flat float32 in the LDS order of mm_linear's B operand: W[k][n] with k = 16 t + 4 g + u,
+    n = 16 nt + i at float index (((t * 8 + nt) * 4 + g) * 16 + i) * 4 + u, so that the 16 lanes (i, g) of one
+    16-byte LDS read take 256 consecutive bytes (no bank conflicts)."""
+    W = W.reshape(8, 4, 4, 8, 16)             # [t, g, u, nt, i]
+    return W.permute(0, 3, 1, 4, 2).reshape(-1).contiguous()
 
 
 def host_ints(vals):
