@@ -67,32 +67,46 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
     return B, F
 
 
-def kernel_digest():
-    """sha256 over the HIP sources of the library (csrc/ and csrc/gen/), to tie measurements to the kernels."""
+# the HIP sources that define each profiled kernel (a measurement stays valid while these are unchanged)
+KERNEL_SOURCES = {
+    "mm_conv2_bwd_kernel": ("gen/conv_l2.hip", "gen/sh.h", "common.h"),
+    "mm_conv2_fwd_kernel": ("gen/conv_l2.hip", "gen/sh.h", "common.h"),
+    "mm_ace1_fwd_kernel": ("ace.hip", "common.h"),
+    "mm_ace1_bwd_kernel": ("ace.hip", "common.h"),
+    "mm_linear_kernel": ("linear.hip", "common.h"),
+    "mm_fill_f32_kernel": ("node.hip", "common.h"),
+    "mm_fill_i32_kernel_nl": ("nlist.hip", "common.h"),
+}
+
+
+def kernel_digest(kernel, read=None):
+    """sha256 over the HIP sources that define `kernel` (paths relative to mace-million_amd/csrc), to tie a
+    measurement to the code it measured.  `read(relpath) -> bytes` defaults to the working tree."""
     import hashlib
-    h = hashlib.sha256()
     base = os.path.join(ROOT, "mace-million_amd", "csrc")
-    for d in (base, os.path.join(base, "gen")):
-        for f in sorted(os.listdir(d)):
-            if f.endswith((".hip", ".h", ".cpp")):
-                with open(os.path.join(d, f), "rb") as fh:
-                    h.update(f.encode() + fh.read())
+    if read is None:
+        def read(rel):
+            with open(os.path.join(base, rel), "rb") as fh:
+                return fh.read()
+    h = hashlib.sha256()
+    for rel in KERNEL_SOURCES[kernel]:
+        h.update(rel.encode() + read(rel))
     return h.hexdigest()
 
 
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this
     workload (profiles/traffic_config5_water1M.json: counters scaled by a copy kernel of known size), or None
-    when no pass was recorded for this workload and these kernel sources."""
+    when no pass was recorded for this workload and the kernel's current sources."""
     path = os.path.join(ROOT, "profiles", "traffic_config5_water1M.json")
-    if not os.path.exists(path):
+    if not os.path.exists(path) or kernel not in KERNEL_SOURCES:
         return None
     with open(path) as fh:
         t = json.load(fh)
-    if (t["workload"] != workload or kernel not in t["kernels"]
-            or t.get("kernel_sources_sha256") != kernel_digest()):
+    rec = t["kernels"].get(kernel)
+    if t["workload"] != workload or rec is None or rec.get("sources_sha256") != kernel_digest(kernel):
         return None
-    return t["kernels"][kernel]["traffic_bytes_per_launch"]
+    return rec["traffic_bytes_per_launch"]
 
 
 def summarize(name, launches, ms_total, B, F, steps):

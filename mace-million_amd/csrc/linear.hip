@@ -6,19 +6,23 @@
 // row lists instead of computing every species and selecting), the product-block linear, and their transposes in
 // the backward passes.  For each output component j of one launch:
 //     out[out_row(r), comp_j] (= or +=) scale(r) * sum_q in[in_row(r), src_{j,q}] @ W[w_{j,q}]
-// Launch: grid (ceil(rows / (64 MT)), n_comp, n_groups); 256 threads = 4 waves, each wave 16 MT rows x 128
-// columns (8 MT MFMA tiles; MT = 2 for large launches); the 128x128 weight block is staged in LDS (64 KiB) in the
-// lane order of the B operand.
+// Launch: grid (ceil(rows / (64 MT n_blk)), n_comp, n_groups); 256 threads = 4 waves, each wave 16 MT rows x 128
+// columns (8 MT MFMA tiles; MT = 2 for large launches) of each of its n_blk row blocks; the 128x128 weight block is
+// staged in LDS (64 KiB) in the lane order of the B operand.
 // Weight blocks are stored pre-permuted: element W[k][n], k = 16 t + 4 g + u, n = 16 nt + i, at float index
 // (((t * 8 + nt) * 4 + g) * 16 + i) * 4 + u, so that lane (i, g) reads its 4 k-values of step t and tile nt as one
 // 16-byte LDS read, the 16 lanes of a group reading 256 consecutive bytes (no bank conflicts), and the A operand of
 // lane (row, g) is the float4 in[row][16 t + 4 g .. + 3].
 #include "common.h"
 
+#include <algorithm>
+
 #define MM_LIN_MAX_COMP 48
 #define MM_LIN_MAX_SRC 3
 // launches with at least this many rows use two M-tiles per wave (128 rows per workgroup)
 #define MM_LIN_MT2_ROWS 8192
+// a launch keeps at least this many workgroups (8 per CU) when it groups row blocks per workgroup
+#define MM_LIN_MIN_WG 2048
 
 struct MMLinComp {
   int n_src;
@@ -47,79 +51,89 @@ struct MMLinArgs {
   MMLinComp comp[MM_LIN_MAX_COMP];
 };
 
-// MT = 16-row M-tiles per wave (rows per workgroup = 64 MT): every B operand read from LDS feeds MT MFMAs.
+// MT = 16-row M-tiles per wave (rows per workgroup block = 64 MT): every B operand read from LDS feeds MT MFMAs.
+// A workgroup handles n_blk consecutive row blocks of one output component; with a single source the weight block
+// is staged in LDS once for all of them.
 template <int MT>
-__global__ void __launch_bounds__(256) mm_linear_kernel(MMLinArgs args) {
+__global__ void __launch_bounds__(256) mm_linear_kernel(MMLinArgs args, int n_blk) {
   __shared__ floatx4 Wl[4096];
   const MMLinComp cp = args.comp[blockIdx.y];
   const int grp = blockIdx.z;
   const int nrows = args.list ? args.list_count[grp] : args.n_rows;
-  const int row0 = blockIdx.x * 64 * MT;
-  if (row0 >= nrows) return;
+  const int blk_rows = 64 * MT;
+  const int blk0 = blockIdx.x * n_blk;
+  if (blk0 * blk_rows >= nrows) return;
+  const int blk1 = min(blk0 + n_blk, (nrows + blk_rows - 1) / blk_rows);
   const int* __restrict__ list = args.list ? args.list + (size_t)grp * args.list_stride : nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
-  bool valid[MT];
-  long in_row[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = row0 + (wave * MT + mt) * 16 + i;
-    valid[mt] = r < nrows;
-    const int rid = valid[mt] ? (list ? list[r] : r) : 0;
-    in_row[mt] = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
-  }
-  floatx4 acc[MT][8];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) acc[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int q = 0; q < cp.n_src; ++q) {
-    const floatx4* __restrict__ Wg =
-        (const floatx4*)(args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 16384);
-    __syncthreads();
-    for (int j = threadIdx.x; j < 4096; j += 256) Wl[j] = Wg[j];
-    __syncthreads();
-    floatx4 a[MT][8];
+  const bool restage = cp.n_src > 1;
+  for (int blk = blk0; blk < blk1; ++blk) {
+    const int row0 = blk * blk_rows;
+    bool valid[MT];
+    long in_row[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const float* __restrict__ ap = args.in + in_row[mt] * args.in_stride + cp.in_off[q] + 4 * g;
-#pragma unroll
-      for (int t = 0; t < 8; ++t)
-        a[mt][t] = valid[mt] ? *(const floatx4*)(ap + 16 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = row0 + (wave * MT + mt) * 16 + i;
+      valid[mt] = r < nrows;
+      const int rid = valid[mt] ? (list ? list[r] : r) : 0;
+      in_row[mt] = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
     }
+    floatx4 acc[MT][8];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        const floatx4 b = Wl[((t * 8 + nt) * 4 + g) * 16 + i];
+      for (int nt = 0; nt < 8; ++nt) acc[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < cp.n_src; ++q) {
+      floatx4 a[MT][8];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].x, b.x, acc[mt][nt], 0, 0, 0);
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].y, b.y, acc[mt][nt], 0, 0, 0);
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].z, b.z, acc[mt][nt], 0, 0, 0);
-          acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].w, b.w, acc[mt][nt], 0, 0, 0);
+      for (int mt = 0; mt < MT; ++mt) {
+        const float* __restrict__ ap = args.in + in_row[mt] * args.in_stride + cp.in_off[q] + 4 * g;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          a[mt][t] = valid[mt] ? *(const floatx4*)(ap + 16 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+      if (restage || blk == blk0) {
+        const floatx4* __restrict__ Wg =
+            (const floatx4*)(args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 16384);
+        __syncthreads();
+        for (int j = threadIdx.x; j < 4096; j += 256) Wl[j] = Wg[j];
+        __syncthreads();
+      }
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          const floatx4 b = Wl[((t * 8 + nt) * 4 + g) * 16 + i];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].x, b.x, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].y, b.y, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].z, b.z, acc[mt][nt], 0, 0, 0);
+            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].w, b.w, acc[mt][nt], 0, 0, 0);
+          }
         }
       }
     }
-  }
-  // D layout of the 16x16 tile: lane (i, g) holds rows 4 g + v (v = 0..3) of column i
+    // D layout of the 16x16 tile: lane (i, g) holds rows 4 g + v (v = 0..3) of column i
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int rr = row0 + (wave * MT + mt) * 16 + 4 * g + v;
-      if (rr >= nrows) continue;
-      const int id = list ? list[rr] : rr;
-      const long orow = args.out_rows ? (long)args.out_rows[id] : (long)id;
-      float s = 1.f;
-      if (args.row_scale) s = args.scale_mode == 1 ? 1.f / (args.row_scale[id] + 1.f) : args.row_scale[id];
-      float* __restrict__ op = args.out + orow * args.out_stride + cp.out_off + i;
+      for (int v = 0; v < 4; ++v) {
+        const int rr = row0 + (wave * MT + mt) * 16 + 4 * g + v;
+        if (rr >= nrows) continue;
+        const int id = list ? list[rr] : rr;
+        const long orow = args.out_rows ? (long)args.out_rows[id] : (long)id;
+        float s = 1.f;
+        if (args.row_scale) s = args.scale_mode == 1 ? 1.f / (args.row_scale[id] + 1.f) : args.row_scale[id];
+        float* __restrict__ op = args.out + orow * args.out_stride + cp.out_off + i;
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        const float val = s * acc[mt][nt][v];
-        if (args.accumulate)
-          op[16 * nt] += val;
-        else
-          op[16 * nt] = val;
+        for (int nt = 0; nt < 8; ++nt) {
+          const float val = s * acc[mt][nt][v];
+          if (args.accumulate)
+            op[16 * nt] += val;
+          else
+            op[16 * nt] = val;
+        }
       }
     }
   }
@@ -164,12 +178,15 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
     a.comp[j].out_off = comp_out_off[j];
   }
   if (n_rows_max == 0) return MM_OK;
-  if (n_rows_max >= MM_LIN_MT2_ROWS) {
-    dim3 grid((n_rows_max + 127) / 128, n_comp, n_groups);
-    hipLaunchKernelGGL(mm_linear_kernel<2>, grid, dim3(256), 0, stream, a);
-  } else {
-    dim3 grid((n_rows_max + 63) / 64, n_comp, n_groups);
-    hipLaunchKernelGGL(mm_linear_kernel<1>, grid, dim3(256), 0, stream, a);
-  }
+  // row blocks per workgroup: as many as keep at least MM_LIN_MIN_WG workgroups in the launch (at most 8)
+  const int mt = n_rows_max >= MM_LIN_MT2_ROWS ? 2 : 1;
+  const long n_blocks = (n_rows_max + 64 * mt - 1) / (64 * mt);
+  const long per_blk = (long)n_comp * n_groups;
+  int n_blk = (int)std::max(1L, std::min(8L, n_blocks * per_blk / MM_LIN_MIN_WG));
+  dim3 grid((unsigned)((n_blocks + n_blk - 1) / n_blk), n_comp, n_groups);
+  if (mt == 2)
+    hipLaunchKernelGGL(mm_linear_kernel<2>, grid, dim3(256), 0, stream, a, n_blk);
+  else
+    hipLaunchKernelGGL(mm_linear_kernel<1>, grid, dim3(256), 0, stream, a, n_blk);
   return mm::launch_status("mm_linear");
 }
