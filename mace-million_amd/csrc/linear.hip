@@ -6,9 +6,9 @@
 // row lists instead of computing every species and selecting), the product-block linear, and their transposes in
 // the backward passes.  For each output component j of one launch:
 //     out[out_row(r), comp_j] (= or +=) scale(r) * sum_q in[in_row(r), src_{j,q}] @ W[w_{j,q}]
-// Launch: grid (ceil(rows / (64 MT n_blk)), n_comp, n_groups); 256 threads = 4 waves, each wave 16 MT rows x 128
-// columns (8 MT MFMA tiles; MT = 2 for large launches) of each of its n_blk row blocks; the 128x128 weight block is
-// staged in LDS (64 KiB) in the lane order of the B operand.
+// Launch: grid (ceil(rows / (128 n_blk)), n_comp, n_groups); 512 threads = 8 waves, each wave 16 rows x 128
+// columns (8 MFMA tiles) of each of its n_blk row blocks; the 128x128 weight block is staged in LDS (64 KiB) in the
+// lane order of the B operand.
 // Weight blocks are stored pre-permuted: element W[k][n], k = 16 t + 4 g + u, n = 16 nt + i, at float index
 // (((t * 8 + nt) * 4 + g) * 16 + i) * 4 + u, so that lane (i, g) reads its 4 k-values of step t and tile nt as one
 // 16-byte LDS read, the 16 lanes of a group reading 256 consecutive bytes (no bank conflicts), and the A operand of
@@ -19,8 +19,11 @@
 
 #define MM_LIN_MAX_COMP 48
 #define MM_LIN_MAX_SRC 3
-// launches with at least this many rows use two M-tiles per wave (128 rows per workgroup)
-#define MM_LIN_MT2_ROWS 8192
+// 8 waves of one 16-row M-tile each: 128 rows per workgroup block.  With the 64 KiB weight block in LDS two
+// workgroups share a CU, i.e. 4 waves per SIMD (measured faster than 4 waves of two M-tiles, 2 waves per SIMD).
+#define MM_LIN_MT 1
+#define MM_LIN_NW 8
+#define MM_LIN_BLOCK_ROWS (16 * MM_LIN_MT * MM_LIN_NW)
 // a launch keeps at least this many workgroups (8 per CU) when it groups row blocks per workgroup
 #define MM_LIN_MIN_WG 2048
 
@@ -51,52 +54,80 @@ struct MMLinArgs {
   MMLinComp comp[MM_LIN_MAX_COMP];
 };
 
-// MT = 16-row M-tiles per wave (rows per workgroup block = 64 MT): every B operand read from LDS feeds MT MFMAs.
-// A workgroup handles n_blk consecutive row blocks of one output component; with a single source the weight block
-// is staged in LDS once for all of them.
 template <int MT>
-__global__ void __launch_bounds__(256) mm_linear_kernel(MMLinArgs args, int n_blk) {
+struct MMLinRows {
+  bool valid[MT];
+  long in_row[MT];
+};
+
+template <int MT>
+__device__ __forceinline__ void mm_lin_rows(const MMLinArgs& args, const int* list, int nrows, int row0, int wave,
+                                            int i, MMLinRows<MT>& rw) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = row0 + (wave * MT + mt) * 16 + i;
+    rw.valid[mt] = r < nrows;
+    const int rid = rw.valid[mt] ? (list ? list[r] : r) : 0;
+    rw.in_row[mt] = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void mm_lin_load_a(const MMLinArgs& args, const MMLinRows<MT>& rw, int in_off, int g,
+                                              floatx4 (&a)[MT][8]) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float* __restrict__ ap = args.in + rw.in_row[mt] * args.in_stride + in_off + 4 * g;
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+      a[mt][t] = rw.valid[mt] ? *(const floatx4*)(ap + 16 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// MT = 16-row M-tiles per wave, NW waves (rows per workgroup block = 16 NW MT): every B operand read from LDS
+// feeds MT MFMAs.
+// A workgroup handles n_blk consecutive row blocks of one output component; with a single source the weight block
+// is staged in LDS once for all of them.  The A operands of the next (block, source) step are loaded while the
+// MFMAs of the current one run.
+template <int MT, int NW>
+__global__ void __launch_bounds__(64 * NW) mm_linear_kernel(MMLinArgs args, int n_blk) {
   __shared__ floatx4 Wl[4096];
   const MMLinComp cp = args.comp[blockIdx.y];
   const int grp = blockIdx.z;
   const int nrows = args.list ? args.list_count[grp] : args.n_rows;
-  const int blk_rows = 64 * MT;
+  const int blk_rows = 16 * NW * MT;
   const int blk0 = blockIdx.x * n_blk;
   if (blk0 * blk_rows >= nrows) return;
   const int blk1 = min(blk0 + n_blk, (nrows + blk_rows - 1) / blk_rows);
   const int* __restrict__ list = args.list ? args.list + (size_t)grp * args.list_stride : nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
-  const bool restage = cp.n_src > 1;
+  const int n_src = cp.n_src;
+  const bool restage = n_src > 1;
+  MMLinRows<MT> rw, rw_next;
+  mm_lin_rows<MT>(args, list, nrows, blk0 * blk_rows, wave, i, rw);
+  floatx4 a[MT][8];
+  mm_lin_load_a<MT>(args, rw, cp.in_off[0], g, a);
   for (int blk = blk0; blk < blk1; ++blk) {
     const int row0 = blk * blk_rows;
-    bool valid[MT];
-    long in_row[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int r = row0 + (wave * MT + mt) * 16 + i;
-      valid[mt] = r < nrows;
-      const int rid = valid[mt] ? (list ? list[r] : r) : 0;
-      in_row[mt] = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
-    }
     floatx4 acc[MT][8];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) acc[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int q = 0; q < cp.n_src; ++q) {
-      floatx4 a[MT][8];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float* __restrict__ ap = args.in + in_row[mt] * args.in_stride + cp.in_off[q] + 4 * g;
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-          a[mt][t] = valid[mt] ? *(const floatx4*)(ap + 16 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < n_src; ++q) {
+      // next step: source q + 1 of this block, else source 0 of the next block
+      floatx4 an[MT][8];
+      const bool next_here = q + 1 < n_src;
+      const bool has_next = next_here || blk + 1 < blk1;
+      if (has_next) {
+        if (!next_here) mm_lin_rows<MT>(args, list, nrows, row0 + blk_rows, wave, i, rw_next);
+        mm_lin_load_a<MT>(args, next_here ? rw : rw_next, cp.in_off[next_here ? q + 1 : 0], g, an);
       }
       if (restage || blk == blk0) {
         const floatx4* __restrict__ Wg =
             (const floatx4*)(args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 16384);
         __syncthreads();
-        for (int j = threadIdx.x; j < 4096; j += 256) Wl[j] = Wg[j];
+        for (int j = threadIdx.x; j < 4096; j += 64 * NW) Wl[j] = Wg[j];
         __syncthreads();
       }
 #pragma unroll
@@ -112,6 +143,12 @@ __global__ void __launch_bounds__(256) mm_linear_kernel(MMLinArgs args, int n_bl
             acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].w, b.w, acc[mt][nt], 0, 0, 0);
           }
         }
+      }
+      if (has_next) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) a[mt][t] = an[mt][t];
       }
     }
     // D layout of the 16x16 tile: lane (i, g) holds rows 4 g + v (v = 0..3) of column i
@@ -136,6 +173,7 @@ __global__ void __launch_bounds__(256) mm_linear_kernel(MMLinArgs args, int n_bl
         }
       }
     }
+    rw = rw_next;
   }
 }
 
@@ -179,14 +217,10 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
   }
   if (n_rows_max == 0) return MM_OK;
   // row blocks per workgroup: as many as keep at least MM_LIN_MIN_WG workgroups in the launch (at most 8)
-  const int mt = n_rows_max >= MM_LIN_MT2_ROWS ? 2 : 1;
-  const long n_blocks = (n_rows_max + 64 * mt - 1) / (64 * mt);
+  const long n_blocks = (n_rows_max + MM_LIN_BLOCK_ROWS - 1) / MM_LIN_BLOCK_ROWS;
   const long per_blk = (long)n_comp * n_groups;
-  int n_blk = (int)std::max(1L, std::min(8L, n_blocks * per_blk / MM_LIN_MIN_WG));
+  const int n_blk = (int)std::max(1L, std::min(8L, n_blocks * per_blk / MM_LIN_MIN_WG));
   dim3 grid((unsigned)((n_blocks + n_blk - 1) / n_blk), n_comp, n_groups);
-  if (mt == 2)
-    hipLaunchKernelGGL(mm_linear_kernel<2>, grid, dim3(256), 0, stream, a, n_blk);
-  else
-    hipLaunchKernelGGL(mm_linear_kernel<1>, grid, dim3(256), 0, stream, a, n_blk);
+  hipLaunchKernelGGL((mm_linear_kernel<MM_LIN_MT, MM_LIN_NW>), grid, dim3(64 * MM_LIN_NW), 0, stream, a, n_blk);
   return mm::launch_status("mm_linear");
 }
