@@ -57,3 +57,19 @@ __device__ __forceinline__ float mm_row_sum16(float v) {
   v += mm_dpp<0x140>(v);   // row_mirror: lane i <- 15 - i: 16-lane sums
   return v;
 }
+
+// Four float adds to LDS (p[0], p[16], p[32], p[48]) through 32-bit compare-and-swap, issued together; a lane
+// repeats only the adds whose swap lost a race.  The native LDS float atomic add (ds_add_f32) runs far below
+// the integer LDS atomics on this GPU (measured), so float sums shared by the waves of a workgroup use this.
+__device__ __forceinline__ void mm_lds_add4_f32(float* p, float v0, float v1, float v2, float v3) {
+  unsigned* u = (unsigned*)p;
+  unsigned a0 = u[0], a1 = u[16], a2 = u[32], a3 = u[48];
+  unsigned r0 = atomicCAS(u, a0, __float_as_uint(__uint_as_float(a0) + v0));
+  unsigned r1 = atomicCAS(u + 16, a1, __float_as_uint(__uint_as_float(a1) + v1));
+  unsigned r2 = atomicCAS(u + 32, a2, __float_as_uint(__uint_as_float(a2) + v2));
+  unsigned r3 = atomicCAS(u + 48, a3, __float_as_uint(__uint_as_float(a3) + v3));
+  while (r0 != a0) { a0 = r0; r0 = atomicCAS(u, a0, __float_as_uint(__uint_as_float(a0) + v0)); }
+  while (r1 != a1) { a1 = r1; r1 = atomicCAS(u + 16, a1, __float_as_uint(__uint_as_float(a1) + v1)); }
+  while (r2 != a2) { a2 = r2; r2 = atomicCAS(u + 32, a2, __float_as_uint(__uint_as_float(a2) + v2)); }
+  while (r3 != a3) { a3 = r3; r3 = atomicCAS(u + 48, a3, __float_as_uint(__uint_as_float(a3) + v3)); }
+}

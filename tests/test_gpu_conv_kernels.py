@@ -1,0 +1,144 @@
+"""The layer-2 edge-convolution kernels (mm_conv2_fwd, mm_conv2_bwd) called through the C ABI on synthetic
+receiver-CSR inputs, against an fp64 autograd restatement of the channelwise tensor product (marked gpu).
+
+Semantics checked (reference kernels K1/K2, conv_spline.py:38-94, 97-181):
+    W[e, w, c]   = a0 + t (a1 + t (a2 + t a3)),   (a0..a3) = table row of edge e, path w, channel c
+    out[i, o, c] = sum_{e: recv(e) = i} sum_terms coef W[e, w, c] X[send(e), k, c] Y[e, m]
+    rho[i]       = sum_{e: recv(e) = i} density(e)
+and, for L = sum gA * out: dL/dX, dL/dY[e, m] and inv_h * dL/dt[e] (the last two summed over the 8 channel
+blocks of the per-edge partials).
+
+The cases drive every path of the backward's accumulation of dL/dX per group of 4 receivers:
+- receivers without edges;
+- a last group of fewer than 4 receivers;
+- groups whose distinct senders exceed the LDS slots;
+- groups with more edges than the per-group edge cap;
+- and local groups that share most senders.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+C = 128
+
+
+def _terms():
+    from mace_onegpu import model as mm
+    return mm.Tables(mm.MaceSpec()).tp2
+
+
+def _case(seed, nC, n_nodes, deg_max, local, NR=9):
+    rng = np.random.default_rng(seed)
+    deg = rng.integers(0, deg_max + 1, nC)
+    deg[::7] = 0
+    send = []
+    for i in range(nC):
+        if local:      # senders in a window around the receiver: neighbouring receivers share them
+            c0 = int(i * n_nodes / nC)
+            lo, hi = max(0, c0 - 80), min(n_nodes, c0 + 80)
+        else:          # senders anywhere: a group's distinct senders overflow the LDS slots
+            lo, hi = 0, n_nodes
+        d = min(int(deg[i]), hi - lo)
+        deg[i] = d
+        send.append(rng.choice(np.arange(lo, hi), d, replace=False))
+    send = np.concatenate(send).astype(np.int32)
+    rowptr = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    E = len(send)
+    u = rng.normal(size=(E, 3))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    r = rng.uniform(0.8, 6.0, E)
+    t = rng.uniform(0.0, 1.0, E)
+    row = rng.integers(0, NR, E)
+    dens = rng.uniform(0.0, 1.0, E)
+    X = rng.normal(size=(n_nodes, 4 * C))
+    tab = rng.normal(size=(8, NR, 10, 16, 4)) * np.array([1.0, 0.5, 0.25, 0.125])
+    gA = rng.normal(size=(nC, 40 * C))
+    return dict(rowptr=rowptr, send=send, u=u, r=r, t=t, row=row, dens=dens, X=X, tab=tab, gA=gA, NR=NR)
+
+
+def _reference(cs, tp):
+    """fp64 forward and autograd backward on the CPU."""
+    from oracle import mace_ref
+    f64 = dict(dtype=torch.float64)
+    E = len(cs["send"])
+    nC = len(cs["rowptr"]) - 1
+    recv = torch.repeat_interleave(torch.arange(nC), torch.from_numpy(np.diff(cs["rowptr"])).long())
+    send = torch.from_numpy(cs["send"]).long()
+    tab = torch.tensor(cs["tab"], **f64).float().double()          # the fp32 table values the kernel reads
+    tabc = tab.permute(1, 2, 0, 3, 4).reshape(cs["NR"], 10, C, 4)  # [row, w, c, coef]
+    t = torch.tensor(cs["t"], **f64).float().double().requires_grad_()
+    Y = mace_ref.sh(torch.tensor(cs["u"], **f64).float().double()).detach().requires_grad_()
+    X = torch.tensor(cs["X"], **f64).float().double().view(-1, 4, C).requires_grad_()
+    a = tabc[torch.from_numpy(cs["row"]).long()]                    # [E, w, c, 4]
+    tt = t[:, None, None]
+    W = a[..., 0] + tt * (a[..., 1] + tt * (a[..., 2] + tt * a[..., 3]))
+    Xs = X[send]                                                    # [E, k, c]
+    by_o = {}
+    for (w, k, m, o, coef) in tp["terms"]:
+        by_o.setdefault(o, []).append((w, k, m, coef))
+    zero = torch.zeros(E, C, **f64)
+    msg = torch.stack([sum((coef * W[:, w] * Xs[:, k] * Y[:, m:m + 1] for (w, k, m, coef) in by_o[o]), zero)
+                       if o in by_o else zero for o in range(40)], 1)
+    out = torch.zeros(nC, 40, C, **f64).index_add(0, recv, msg)
+    rho = torch.zeros(nC, **f64).index_add(0, recv, torch.tensor(cs["dens"], **f64).float().double())
+    gA = torch.tensor(cs["gA"], **f64).float().double().view(nC, 40, C)
+    (out * gA).sum().backward()
+    return out.detach(), rho, X.grad.reshape(-1, 4 * C), Y.grad, t.grad
+
+
+@pytest.mark.parametrize("name,nC,n_nodes,deg_max,local", [
+    ("local", 203, 1500, 120, True),        # 203 = 50 groups of 4 + a group of 3
+    ("scattered", 97, 4000, 240, False),    # distinct senders per group > slots; edges per group > cap
+    ("sparse", 61, 300, 6, False),          # few edges, many empty receivers
+])
+def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local):
+    from mace_onegpu._lib import K, stream
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    tp = _terms()
+    cs = _case(7, nC, n_nodes, deg_max, local)
+    E = len(cs["send"])
+    print(f"case {name}: nC {nC} nodes {n_nodes} edges {E}", flush=True)
+    dev = "cuda"
+    f32 = dict(dtype=torch.float32, device=dev)
+    pk = torch.empty(E, 4, **f32)
+    pk[:, 0] = torch.tensor(cs["t"], **f32)
+    pk[:, 3] = torch.tensor(cs["dens"], **f32)
+    pki = pk.view(torch.int32)
+    pki[:, 1] = torch.tensor(cs["row"], dtype=torch.int32, device=dev)
+    pki[:, 2] = torch.tensor(cs["send"], dtype=torch.int32, device=dev)
+    eu = torch.empty(E, 4, **f32)
+    eu[:, :3] = torch.tensor(cs["u"], **f32)
+    eu[:, 3] = torch.tensor(cs["r"], **f32)
+    rowptr = torch.tensor(cs["rowptr"], dtype=torch.int32, device=dev)
+    X = torch.tensor(cs["X"], **f32)
+    tab = torch.tensor(cs["tab"], **f32).contiguous()
+    gA = torch.tensor(cs["gA"], **f32)
+    out = torch.full((nC, 40 * C), float("nan"), **f32)
+    rho = torch.full((nC,), float("nan"), **f32)
+    inv_h = 3.0
+    part = torch.full((8, E * 17 + 5), float("nan"), **f32)
+    gX = torch.zeros(n_nodes, 4 * C, **f32)
+    M = cs["NR"] + 1
+    K.mm_conv2_fwd(rowptr, nC, pk, eu, X, 4 * C, tab, 1, M, out, rho, stream())
+    K.mm_conv2_bwd(rowptr, nC, pk, eu, X, 4 * C, tab, 1, M, inv_h, gA, part, E * 17 + 5, gX, stream())
+    torch.cuda.synchronize()
+    out_r, rho_r, gX_r, gY_r, gt_r = _reference(cs, tp)
+
+    def close(name, got, ref, rel):
+        got = got.double().cpu()
+        err = float((got - ref).abs().max())
+        scale = float(ref.abs().max())
+        print(f"  {name}: max|err| {err:.3e} (max|ref| {scale:.3e})", flush=True)
+        assert torch.isfinite(got).all() and err <= rel * scale + 1e-12
+
+    # fp32 sums of at most a few thousand products against fp64: 1e-5 of the largest value (an indexing or
+    # race error is of the order of the values themselves)
+    close("out", out.view(nC, 40, C), out_r, 1e-5)
+    close("rho", rho, rho_r, 1e-5)
+    close("gX", gX, gX_r, 1e-5)
+    p = part[:, :E * 17].view(8, E, 17).double().sum(0).cpu()
+    close("dL/dY", p[:, 1:], gY_r, 1e-5)
+    close("inv_h dL/dt", p[:, 0], inv_h * gt_r, 1e-5)
+    assert torch.isnan(part[:, E * 17:]).all()      # nothing written past the partials
