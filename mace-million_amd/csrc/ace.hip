@@ -37,15 +37,22 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[s][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float dsum = 0.f;
+  // the packed record and harmonic of the next step are loaded one step ahead
+  floatx4 pk_n = e0 + g < e1 ? e_pk[e0 + g] : floatx4{0.f, 0.f, 0.f, 0.f};
+  float y_n = e0 + g < e1 ? e_Y[(size_t)(e0 + g) * 16 + i16] : 0.f;
   for (int kb = e0; kb < e1; kb += 4) {
     const int e = kb + g;
     const bool valid = e < e1;
-    const floatx4 pk = valid ? e_pk[e] : floatx4{0.f, 0.f, 0.f, 0.f};
-    const float y = valid ? e_Y[(size_t)e * 16 + i16] : 0.f;
+    const floatx4 pk = pk_n;
+    const float y = valid ? y_n : 0.f;
+    if (e + 4 < e1) {
+      pk_n = e_pk[e + 4];
+      y_n = e_Y[(size_t)(e + 4) * 16 + i16];
+    }
     const int se = valid ? __float_as_int(pk.z) : -1;
     const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
     const float t = pk.x;
-    if (i16 == 0) dsum += pk.w;
+    if (i16 == 0 && valid) dsum += pk.w;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const floatx4 c = tp[16 * mt];
@@ -87,10 +94,19 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int k = 0; k < 16; ++k) gb[s][k] = gp[s * MM_ACE_H + 4 * k];
+  // the packed record of the next tile is loaded one tile ahead; the tile's harmonics before its MFMAs
+  floatx4 pk_n = e0 + i16 < e1 ? e_pk[e0 + i16] : floatx4{0.f, 0.f, 0.f, 0.f};
   for (int tb = e0; tb < e1; tb += 16) {
     const int e = tb + i16;          // A-operand row: edge i16 of the tile
     const bool valid = e < e1;
-    const floatx4 pk = valid ? e_pk[e] : floatx4{0.f, 0.f, 0.f, 0.f};
+    const floatx4 pk = pk_n;
+    if (e + 16 < e1) pk_n = e_pk[e + 16];
+    float yv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int ev = tb + 4 * g + v;
+      yv[v] = ev < e1 ? e_Y[(size_t)ev * 16 + i16] : 0.f;
+    }
     const int se = valid ? __float_as_int(pk.z) : -1;
     const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + g;
     const float t = pk.x;
@@ -111,8 +127,7 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
     for (int v = 0; v < 4; ++v) {
       const int ev = tb + 4 * g + v;
       const bool ok = ev < e1;
-      const float y = ok ? e_Y[(size_t)ev * 16 + i16] : 0.f;
-      const float gr = mm_row_sum16(dYp[v] * y);
+      const float gr = mm_row_sum16(dYp[v] * yv[v]);
       if (ok) {
         float* __restrict__ pp = part + (size_t)ev * 17;
         pp[1 + i16] = dY[v];
