@@ -143,12 +143,13 @@ class ThreePassMLIAP(MLIAPUnified):
             torch.cuda.empty_cache()
             margin = float(os.environ.get("MACE3P_CAP_MARGIN", "1.25"))
             n_cap, e_cap, nt_cap = chunk_graphs.capacities(n_max, e_max, nt, self.e_align, margin)
-            gx = chunk_graphs.ChunkGraphExec(self._fl, self.chunk, n_cap, e_cap, nt_cap, "rij", self._cache_l1)
-            gx.capture(full[0])
+            gx = chunk_graphs.ChunkGraphExec(self._fl, self.chunk, n_cap, e_cap, nt_cap, "rij", self._cache_l1,
+                                             exchange=True)
             self._gx = gx
             self.n_captures = getattr(self, "n_captures", 0) + 1
             if self._log is not None:
                 self._log.write(json.dumps(dict(capture=dict(n_cap=n_cap, e_cap=e_cap, nt_cap=nt_cap))) + "\n")
+        gx.begin(graphs)
         return gx
 
     def _topology_all(self, bounds, rp_cpu, pi, pj, nl, nt):
@@ -209,19 +210,24 @@ class ThreePassMLIAP(MLIAPUnified):
         gx = self._prepare_graphs(graphs, nt) if self._use_graphs else None
         torch.cuda.synchronize()
         t["A_topology"] = time.perf_counter() - t0
-        eat = torch.zeros(nl, dtype=torch.float64, device=dev)
         PF = torch.zeros(P, 3, dtype=torch.float32, device=dev)
         # ---------------- pass A
         t0 = time.perf_counter()
-        H1 = torch.zeros(nt, D1, dtype=torch.float32, device=dev)
         cache = None
-        if self._cache_l1:
-            if self._l1cache is None or self._l1cache["rho"].numel() < nl:
-                self._l1cache = fl.layer1_cache(nl)
-            cache = self._l1cache
+        if gx is not None:      # the executor's static buffers: its graphs read and write them in place
+            H1, eat = gx.H1[:nt], gx.eat[:nl]
+            H1.zero_()
+            cache = gx.cache()
+        else:
+            H1 = torch.zeros(nt, D1, dtype=torch.float32, device=dev)
+            eat = torch.zeros(nl, dtype=torch.float64, device=dev)
+            if self._cache_l1:
+                if self._l1cache is None or self._l1cache["rho"].numel() < nl:
+                    self._l1cache = fl.layer1_cache(nl)
+                cache = self._l1cache
         for g in graphs:
             if gx is not None and g.nC == C:
-                gx.pass_a(g, H1, cache)
+                gx.pass_a(g)
             else:
                 fl.pass_a(g, H1, cache)
         H1x = gx.H1x[:nt] if gx is not None else torch.empty_like(H1)
@@ -234,16 +240,17 @@ class ThreePassMLIAP(MLIAPUnified):
         if gx is not None:
             G1 = gx.G1[:nt]
             G1.zero_()
+            eat.zero_()
         else:
             G1 = torch.zeros_like(H1x)
         for g in graphs:
             if gx is not None and g.nC == C:
-                gx.pass_b(g, PF, eat)
+                gx.pass_b(g)
             else:
                 fl.pass_b(g, H1x, G1, PF, eat)
         H1c = H1x if cache is not None else None       # pass C reads h1 from H1x only with the layer-1 cache
         del H1x
-        G1r = torch.empty_like(G1)
+        G1r = gx.G1r[:nt] if gx is not None else torch.empty_like(G1)
         _exchange(data.reverse_exchange, G1, G1r, D1)
         del G1
         torch.cuda.synchronize()
@@ -252,15 +259,17 @@ class ThreePassMLIAP(MLIAPUnified):
         t0 = time.perf_counter()
         for g in graphs:
             if gx is not None and g.nC == C:
-                gx.pass_c(g, G1r, PF, eat, H1c, cache)
+                gx.pass_c(g)
             elif cache is None:
                 fl.pass_c(g, G1r, PF, eat)
             else:
                 fl.pass_c(g, G1r, PF, eat, H1c, cache)
+        if gx is not None:
+            gx.finish(graphs, PF)
         del G1r, H1c
         torch.cuda.synchronize()
         t["C"] = time.perf_counter() - t0
-        eat += self._e0[elems[:nl]] + self.shift
+        eat = eat + self._e0[elems[:nl]] + self.shift
         PF = PF.double()
         if order is not None:
             out = torch.empty_like(PF)

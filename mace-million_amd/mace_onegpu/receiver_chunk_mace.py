@@ -182,6 +182,8 @@ class ReceiverChunkMACE:
         return out
 
     def _graph_exec(self, fl, sysm, graphs):
+        """The HIP-graph executor of this call's full chunks, their topology loaded (a new executor -- new
+        captures -- when the box changes or a capacity is exceeded); None without full chunks."""
         from . import chunk_graphs
         full = [g for g in graphs if g.nC == self.chunk]
         if not full:
@@ -197,11 +199,10 @@ class ReceiverChunkMACE:
             gx = chunk_graphs.ChunkGraphExec(fl, self.chunk, n_cap, e_cap, nt_cap, "pos", self.cache_layer1,
                                              box_host=host_f64(box))
             gx.box = box
-            gx.set_positions(sysm.pos)
-            gx.capture(full[0])
             self._gx = gx
             self.n_captures += 1
         gx.set_positions(sysm.pos)
+        gx.begin(graphs)
         return gx
 
     def compute(self, sysm, graphs=None, timings=None):
@@ -215,19 +216,20 @@ class ReceiverChunkMACE:
         t0 = time.perf_counter()
         gx = self._graph_exec(fl, sysm, graphs) if self.use_graphs else None
         nC = self.chunk
-        if gx is not None:
-            H1, G1 = gx.H1x[:N], gx.G1[:N]
+        cache = None
+        if gx is not None:      # the executor's static buffers: its graphs read and write them in place
+            H1, G1, eat = gx.H1x[:N], gx.G1[:N], gx.eat[:N]
             H1.zero_()
+            cache = gx.cache()
         else:
             H1 = torch.zeros(N, self.D1, dtype=torch.float32, device=dev)
-        cache = None
-        if self.cache_layer1:
-            if self._cache is None or self._cache["rho"].numel() < N:
-                self._cache = fl.layer1_cache(N)
-            cache = self._cache
+            if self.cache_layer1:
+                if self._cache is None or self._cache["rho"].numel() < N:
+                    self._cache = fl.layer1_cache(N)
+                cache = self._cache
         for g in graphs:
             if gx is not None and g.nC == nC:
-                gx.pass_a(g, H1, cache)
+                gx.pass_a(g)
             else:
                 fl.pass_a(g, H1, cache)
         torch.cuda.synchronize()
@@ -235,13 +237,14 @@ class ReceiverChunkMACE:
         t0 = time.perf_counter()
         if gx is not None:
             G1.zero_()
+            eat.zero_()
         else:
             G1 = torch.zeros_like(H1)
+            eat = torch.zeros(N, dtype=torch.float64, device=dev)
         PF = torch.zeros(max(E, 1), 3, dtype=torch.float32, device=dev)
-        eat = torch.zeros(N, dtype=torch.float64, device=dev)
         for g in graphs:
             if gx is not None and g.nC == nC:
-                gx.pass_b(g, PF, eat)
+                gx.pass_b(g)
             else:
                 fl.pass_b(g, H1, G1, PF, eat)
         torch.cuda.synchronize()
@@ -249,12 +252,14 @@ class ReceiverChunkMACE:
         t0 = time.perf_counter()
         for g in graphs:
             if gx is not None and g.nC == nC:
-                gx.pass_c(g, G1, PF, eat, H1, cache)
+                gx.pass_c(g)
             else:
                 fl.pass_c(g, G1, PF, eat, H1, cache)
+        if gx is not None:
+            gx.finish(graphs, PF)
         torch.cuda.synchronize()
         t["C"] = time.perf_counter() - t0
-        eat += fl.e0[sysm.spidx.long()] + fl.shift
+        eat = eat + fl.e0[sysm.spidx.long()] + fl.shift
         F = pair_to_atom_forces(sysm, PF)
         if timings is not None:
             timings.update(t)
