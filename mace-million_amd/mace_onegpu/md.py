@@ -43,7 +43,8 @@ class PairList:
         r2 = self.r_max ** 2
         K.mm_nl_filter_count(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.NN, stream())
         K.mm_nl_scan(self.NN, self.rowptr, self.N, s._ws, s._ws.numel(), stream())
-        E = int(self.rowptr[-1])
+        self.rp_cpu = self.rowptr.cpu().numpy()          # the one device-to-host read of a step
+        E = int(self.rp_cpu[-1])
         if self.send is None or self.send.numel() < E:
             self.send = torch.empty(int(E * 1.1) + 1, dtype=torch.int32, device=self.device)
         K.mm_nl_filter_fill(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.rowptr, self.send, self.fidx,
@@ -51,6 +52,51 @@ class PairList:
         self.E = E
         self.send_view = self.send[:E]
         return E
+
+    def chunk_graphs(self, chunk, col2s):
+        """Chunks of the current filtered pairs for ReceiverChunkMACE, without per-chunk device-to-host reads.
+
+        The node list of a chunk (its receivers, then the senders outside it in ascending order, as
+        chunk_topology builds it) is taken from the SKIN list once per neighbour-list rebuild: a superset of the
+        senders of every filtered list until the next rebuild.  Rows of senders that no filtered edge uses are
+        computed and never read.  Per step, the local sender index of every filtered edge is one gather,
+        loc[chunk(recv), send]; the chunk objects (and the species lists FastLayers keeps on them) persist."""
+        from .receiver_chunk_mace import chunk_topology, ChunkGraph
+        dev, N = self.device, self.N
+        key = (int(chunk), col2s.data_ptr())      # col2s: model column -> compact species of the layers
+        if getattr(self, "_tmpl_key", None) != key:
+            s = self._skin
+            node_spec_all = col2s[self.spidx.long()]
+            rp_s = s.rowptr.cpu().numpy()
+            loc = torch.full((N,), -1, dtype=torch.int32, device=dev)
+            flag = torch.zeros(N, dtype=torch.bool, device=dev)
+            n_chunks = (N + chunk - 1) // chunk
+            self._loc2d = torch.full((n_chunks, N), -1, dtype=torch.int32, device=dev)
+            self._tmpl = []
+            for c, a in enumerate(range(0, N, chunk)):
+                b = min(a + chunk, N)
+                nodes, _ = chunk_topology(a, b, int(rp_s[a]), int(rp_s[b]), s.send, loc, flag)
+                self._loc2d[c, nodes.long()] = torch.arange(nodes.numel(), device=dev, dtype=torch.int32)
+                g = ChunkGraph()
+                g.a, g.b, g.nC = a, b, b - a
+                g.nodes = nodes.contiguous()
+                g.n_nodes = nodes.numel()
+                g.node_spec = node_spec_all[g.nodes.long()].contiguous()
+                self._tmpl.append(g)
+            self._tmpl_key = key
+        E = self.E
+        recv = torch.repeat_interleave(torch.arange(N, device=dev, dtype=torch.int32), self.NN, output_size=E)
+        # n_chunks * N < 2^31 for any system this driver holds: int32 flat index into loc
+        ls_all = torch.index_select(self._loc2d.view(-1), 0, (recv // chunk) * N + self.send_view)
+        rp = self.rp_cpu
+        for g in self._tmpl:
+            e0, e1 = int(rp[g.a]), int(rp[g.b])
+            g.e0, g.e1, g.nE = e0, e1, e1 - e0
+            g.ls = ls_all[e0:e1]
+            g.rowptr = (self.rowptr[g.a:g.b + 1] - e0).to(torch.int32)
+            g.recv_local = recv[e0:e1] - g.a
+            g.pos, g.box_host = self.pos, self._box_h
+        return self._tmpl
 
     def atom_forces(self, PF):
         """F_i = -sum_{pairs (i, j)} PF + sum_{pairs (j, i)} PF of the current filtered list (fp64)."""
@@ -148,3 +194,4 @@ class _PairView:
         self.N, self.device, self.box, self.pos, self.spidx = pl.N, pl.device, pl.box, pl.pos, pl.spidx
         self.NN, self.rowptr, self.send = pl.NN, pl.rowptr, pl.send_view
         self.atom_forces_fn = pl.atom_forces
+        self.chunk_graphs = pl.chunk_graphs

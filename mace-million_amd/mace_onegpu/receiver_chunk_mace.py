@@ -154,14 +154,21 @@ class ReceiverChunkMACE:
 
     def _layers(self, sysm):
         from .fast_layers import FastLayers
+        key = (sysm.spidx.data_ptr(), sysm.spidx.numel(), sysm.spidx._version)
+        if self.fl is not None and getattr(self, "_cols_key", None) == key:
+            return self.fl          # same species array as the last call: no device-to-host read
         cols = sorted(int(c) for c in torch.unique(sysm.spidx.long()).tolist())
         if self.fl is None or self.fl.cols != cols:
             self.fl = FastLayers(self.model, cols, self.spline_grid, device=self.dev, ace_layer1=self.ace_layer1)
+        self._cols_key = key
         return self.fl
 
     def graphs(self, sysm):
-        """Topologies of all chunks (cached per neighbour list)."""
+        """Topologies of all chunks (a pair list that builds its own chunks -- the MD driver's -- is asked for
+        them)."""
         fl = self._layers(sysm)
+        if getattr(sysm, "chunk_graphs", None) is not None:
+            return sysm.chunk_graphs(self.chunk, fl.col2s)
         dev, N = self.dev, sysm.N
         rp = sysm.rowptr
         rp_cpu = rp.cpu().numpy()
@@ -210,9 +217,10 @@ class ReceiverChunkMACE:
         fl = self._layers(sysm)
         dev, N = self.dev, sysm.N
         graphs = graphs if graphs is not None else self.graphs(sysm)
-        E = int(sysm.rowptr[-1])
+        E = sum(g.nE for g in graphs)
         t = {}
-        torch.cuda.synchronize()
+        sync = torch.cuda.synchronize if timings is not None else (lambda: None)   # pass timings only on request
+        sync()
         t0 = time.perf_counter()
         gx = self._graph_exec(fl, sysm, graphs) if self.use_graphs else None
         nC = self.chunk
@@ -232,7 +240,7 @@ class ReceiverChunkMACE:
                 gx.pass_a(g)
             else:
                 fl.pass_a(g, H1, cache)
-        torch.cuda.synchronize()
+        sync()
         t["A"] = time.perf_counter() - t0
         t0 = time.perf_counter()
         if gx is not None:
@@ -247,7 +255,7 @@ class ReceiverChunkMACE:
                 gx.pass_b(g)
             else:
                 fl.pass_b(g, H1, G1, PF, eat)
-        torch.cuda.synchronize()
+        sync()
         t["B"] = time.perf_counter() - t0
         t0 = time.perf_counter()
         for g in graphs:
@@ -257,7 +265,7 @@ class ReceiverChunkMACE:
                 fl.pass_c(g, G1, PF, eat, H1, cache)
         if gx is not None:
             gx.finish(graphs, PF)
-        torch.cuda.synchronize()
+        sync()
         t["C"] = time.perf_counter() - t0
         eat = eat + fl.e0[sysm.spidx.long()] + fl.shift
         F = pair_to_atom_forces(sysm, PF)

@@ -351,6 +351,32 @@ def test_fmax_guard_raises(dev, model, water_gpu, monkeypatch):
     assert data.pair_forces is None
 
 
+def test_md_chunks_from_skin_list_match_per_call_topology(dev, model):
+    """The MD pair list's chunks (node lists from the skin list, built once per rebuild; local senders by one
+    gather per step) give the energies and pair forces of the per-call chunk topology (chunk_topology) on the same
+    filtered pairs, over several steps and a rebuild; only the fp32 atomic order differs."""
+    from mace_onegpu import systems
+    from mace_onegpu.md import MDRunner, _PairView
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
+    pos, box, Z = systems.water_box(512, seed=3)
+    md = MDRunner(model, pos, box, Z, chunk=700, device=dev)             # 1536 atoms: 2 full chunks + a tail
+    ref = ReceiverChunkMACE(model, chunk=700, device=dev)
+    for step in range(4):
+        if step == 2:
+            md._build(md.pos.clone())                     # a neighbour-list rebuild: new skin list, new chunks
+        md.step()
+        view = _PairView(md.pairs)
+        E1, eat1, F1, PF1 = md.ev.compute(view)
+        view.chunk_graphs = None                          # the generic per-call topology on the same pairs
+        E0, eat0, F0, PF0 = ref.compute(view)
+        n_nodes = [g.n_nodes for g in md.pairs._tmpl]
+        dP = float((PF1 - PF0).abs().max())
+        _say(f"  step {step} (rebuilds {md.n_rebuild}): nodes {n_nodes}, |dE| {abs(E1 - E0):.2e}, max|dPF| {dP:.2e}")
+        assert abs(E1 - E0) < 1e-9 * len(pos) and float((eat1 - eat0).abs().max()) < 1e-9
+        assert dP <= 1e-6 * float(PF0.abs().max())
+    assert md.n_rebuild >= 2
+
+
 def test_md_skin_forces_match_sorted_sum(dev, model):
     """Per-atom forces of an MD step summed through the skin list's reverse-pair map (mm_pair_forces_skin) equal
     the receiver + sender-sorted sums of mm_pair_forces_to_atoms for the same pair forces."""
