@@ -84,6 +84,26 @@ def test_topology_matches_reference(ci):
     assert np.array_equal(np.concatenate(ls_all), T[f"c{ci}__ls"])
 
 
+@pytest.mark.parametrize("ci", [0, 1, 2])
+def test_product_chunk_topology_matches_reference(ci):
+    """The product's chunk builder (receiver_chunk_mace.chunk_topology, as the standalone, ML-IAP and MD paths
+    call it) reproduces the reference's golden nodes and local sender indices (plain torch, run here on the
+    CPU), and restores its scratch arrays."""
+    import torch
+    from mace_onegpu.receiver_chunk_mace import chunk_topology
+    pi, pj = T[f"c{ci}__pi"], T[f"c{ci}__pj"]
+    nl, nt, C = (int(x) for x in T[f"c{ci}__meta"])
+    rp = np.searchsorted(pi, np.arange(nl + 1))
+    pj_t = torch.as_tensor(pj.astype(np.int32))
+    loc = torch.full((nt,), -1, dtype=torch.int32)
+    flag = torch.zeros(nt, dtype=torch.bool)
+    topo = [chunk_topology(a, min(a + C, nl), int(rp[a]), int(rp[min(a + C, nl)]), pj_t, loc, flag)
+            for a in range(0, nl, C)]
+    assert np.array_equal(torch.cat([n for n, _ in topo]).numpy(), T[f"c{ci}__nodes"])
+    assert np.array_equal(torch.cat([l for _, l in topo]).numpy(), T[f"c{ci}__ls"])
+    assert bool((loc == -1).all()) and not bool(flag.any())
+
+
 def test_reverse_pairs_map():
     """reverse_pairs (the MD force sum's reverse-pair map) is an involution mapping (i, j) to (j, i)."""
     import torch
