@@ -122,3 +122,18 @@ def test_symmetric_contraction_basis_spans_the_equivariant_space(L):
     paths = o3.symmetric_contraction_paths([0, 1, 2, 3], L, 3)
     for nu in (1, 2, 3):
         assert len(paths[nu]) == _equivariant_dim(nu, L), (L, nu)
+
+
+def test_unnormalised_harmonic_polynomials():
+    """The backward edge convolution evaluates P_m (mm_shp16) and folds c_m into its coefficients:
+    c_m P_m(u) = Y_m(u) on unit vectors, and the generated 1 / c_m table matches."""
+    import re
+    from mace_onegpu import codegen
+    rng = np.random.default_rng(5)
+    u = rng.normal(size=(200, 3))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    Y = np.stack(o3.sh_cartesian(u[:, 0], u[:, 1], u[:, 2]), 1)
+    P = np.stack(codegen._sh_poly(u[:, 0], u[:, 1], u[:, 2]), 1)
+    assert np.abs(P * np.asarray(codegen.SH_NORM) - Y).max() < 1e-12
+    inv = [float(v) for v in re.findall(r"r = m == \d+ \? ([0-9.e+-]+)f", codegen.sh_header())]
+    assert np.allclose(inv, 1.0 / np.asarray(codegen.SH_NORM)[1:], rtol=1e-15)
