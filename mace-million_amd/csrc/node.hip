@@ -115,38 +115,67 @@ extern "C" int mm_readout1(int n, const float* h1, long h_stride, const float* w
 }
 
 // R2(h2) = sum_j w2_j silu_n(h2 . W1[:, j]) with W1 = r1_w1 / sqrt(C), w2 = r1_w2 / sqrt(16), silu_n = cst silu;
-// eat[i] += scale R2_i;  g_h2[i] = scale dR2/dh2.  One wave per node, hidden width H <= 64.
-__global__ void mm_readout2_kernel(int n, const float* __restrict__ h2, long h_stride, const float* __restrict__ W1,
-                                   const float* __restrict__ w2, int H, float cst, float scale,
-                                   double* __restrict__ eat, float* __restrict__ gh, long gh_stride) {
-  const int node = blockIdx.x * 4 + (threadIdx.x >> 6);
+// eat[i] += scale R2_i;  g_h2[i] = scale dR2/dh2.
+// One thread per node (hidden width H <= MM_RO2_HMAX): the weights are read at the same address by every lane
+// (scalar loads), the node's 128 features stream in as float4 and the gradient row goes out as float4.
+#define MM_RO2_HMAX 32
+__global__ void __launch_bounds__(256) mm_readout2_kernel(int n, const float* __restrict__ h2, long h_stride,
+                                                          const float* __restrict__ W1, const float* __restrict__ w2,
+                                                          int H, float cst, float scale, double* __restrict__ eat,
+                                                          float* __restrict__ gh, long gh_stride) {
+  const int node = blockIdx.x * blockDim.x + threadIdx.x;
   if (node >= n) return;
-  const int lane = threadIdx.x & 63;
-  const float* __restrict__ hp = h2 + (size_t)node * h_stride;
-  const float a0 = hp[lane], a1 = hp[lane + 64];
-  float e = 0.f, g0 = 0.f, g1 = 0.f;
-  for (int j = 0; j < H; ++j) {
-    const float wa = W1[lane * H + j], wb = W1[(lane + 64) * H + j];
-    float z = a0 * wa + a1 * wb;
-    for (int o = 32; o >= 1; o >>= 1) z += __shfl_xor(z, o);   // every lane holds the full z_j
-    const float sg = 1.f / (1.f + expf(-z));
-    e += w2[j] * cst * z * sg;
-    const float gz = scale * w2[j] * cst * sg * (1.f + z * (1.f - sg));   // scale * d/dz (w2_j cst silu(z))
-    g0 = fmaf(gz, wa, g0);
-    g1 = fmaf(gz, wb, g1);
+  const floatx4* __restrict__ hp = (const floatx4*)(h2 + (size_t)node * h_stride);
+  float z[MM_RO2_HMAX];
+#pragma unroll
+  for (int j = 0; j < MM_RO2_HMAX; ++j) z[j] = 0.f;
+  for (int c4 = 0; c4 < MM_C / 4; ++c4) {
+    const floatx4 a = hp[c4];
+    const float* __restrict__ wr = W1 + (size_t)(4 * c4) * H;
+#pragma unroll
+    for (int j = 0; j < MM_RO2_HMAX; ++j) {
+      if (j < H) {
+        z[j] = fmaf(a.x, wr[j], z[j]);
+        z[j] = fmaf(a.y, wr[H + j], z[j]);
+        z[j] = fmaf(a.z, wr[2 * H + j], z[j]);
+        z[j] = fmaf(a.w, wr[3 * H + j], z[j]);
+      }
+    }
   }
-  if (lane == 0) eat[node] += (double)(scale * e);
-  float* __restrict__ op = gh + (size_t)node * gh_stride;
-  op[lane] = g0;
-  op[lane + 64] = g1;
+  float e = 0.f;
+#pragma unroll
+  for (int j = 0; j < MM_RO2_HMAX; ++j) {
+    if (j < H) {
+      const float sg = 1.f / (1.f + expf(-z[j]));
+      e += w2[j] * cst * z[j] * sg;
+      z[j] = scale * w2[j] * cst * sg * (1.f + z[j] * (1.f - sg));   // scale * d/dz (w2_j cst silu(z))
+    }
+  }
+  eat[node] += (double)(scale * e);
+  floatx4* __restrict__ op = (floatx4*)(gh + (size_t)node * gh_stride);
+  for (int c4 = 0; c4 < MM_C / 4; ++c4) {
+    const float* __restrict__ wr = W1 + (size_t)(4 * c4) * H;
+    floatx4 g = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < MM_RO2_HMAX; ++j) {
+      if (j < H) {
+        g.x = fmaf(z[j], wr[j], g.x);
+        g.y = fmaf(z[j], wr[H + j], g.y);
+        g.z = fmaf(z[j], wr[2 * H + j], g.z);
+        g.w = fmaf(z[j], wr[3 * H + j], g.w);
+      }
+    }
+    op[c4] = g;
+  }
 }
 
 extern "C" int mm_readout2(int n, const float* h2, long h_stride, const float* W1, const float* w2, int H,
                            float cst, float scale, double* eat, float* gh, long gh_stride, hipStream_t stream) {
-  MM_CHECK_ARG(n >= 0 && H >= 1 && H <= 64, "bad sizes");
+  MM_CHECK_ARG(n >= 0 && H >= 1 && H <= MM_RO2_HMAX, "bad sizes (1 <= H <= 32)");
+  MM_CHECK_ARG(h_stride % 4 == 0 && gh_stride % 4 == 0, "row strides must be multiples of 4 floats");
   if (n == 0) return MM_OK;
-  hipLaunchKernelGGL(mm_readout2_kernel, dim3((n + 3) / 4), dim3(256), 0, stream, n, h2, h_stride, W1, w2, H, cst,
-                     scale, eat, gh, gh_stride);
+  hipLaunchKernelGGL(mm_readout2_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, n, h2, h_stride, W1, w2, H,
+                     cst, scale, eat, gh, gh_stride);
   return mm::launch_status("mm_readout2");
 }
 
