@@ -1,5 +1,5 @@
 #!/usr/bin/env python
-"""Benchmark of the MI355X three-pass MACE path on one GPU.
+"""Benchmark of the MI355X three-pass MACE path on one GPU (benchmark configurations 2-5).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5|4|3|2] [--no-cpu] [--graphs]
 

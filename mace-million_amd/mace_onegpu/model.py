@@ -20,9 +20,10 @@ architecture is restated here from its definition (block types asserted at fast_
 
 Normalisations follow e3nn's conventions (weights ~ N(0, 1); Linear: 1/sqrt(fan_in) summed over the paths
 into one output; FullyConnectedNet: h <- silu_n(h @ W / sqrt(fan_in)) with silu_n = normalize2mom(silu);
-FullyConnectedTensorProduct with a one-hot: 1/sqrt(mul_in * n_el)).  Choices that BASELINE leaves open and this
-build fixes: no Agnesi distance transform, no ZBL pair repulsion, the cutoff multiplies the radial-MLP output and
-the density (mace's ``cutoff is not None`` branch, fast_layers.py:190-192), silu_n's constant by quadrature.
+FullyConnectedTensorProduct with a one-hot: 1/sqrt(mul_in * n_el)).  Choices the benchmark specification leaves
+open and this build fixes: no Agnesi distance transform, no ZBL pair repulsion, the cutoff multiplies the
+radial-MLP output and the density (mace's ``cutoff is not None`` branch, fast_layers.py:190-192), silu_n's
+constant by quadrature.
 Features are stored "ir_mul" (component-major, channel-minor), as in the reference (make_threepass_model.py:42).
 """
 import math
@@ -42,7 +43,7 @@ HIDDEN_OUT2 = [0]          # h2: 128x0e
 
 
 class MaceSpec:
-    """Architecture of the random-init "MPA-0-medium" model."""
+    """Architecture of the random-init "MPA-0-medium" model of the benchmark configurations."""
 
     def __init__(self, num_elements=89, C=128, r_max=6.0, num_bessel=8, p_cutoff=5, radial_mlp=(64, 64, 64),
                  correlation=3, mlp_irreps=16, scale=1.0, shift=0.0):

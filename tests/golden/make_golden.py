@@ -2,7 +2,7 @@
 
 Run in the build container only (needs /root/reference, read-only; torch + numpy):
     python tests/golden/make_golden.py
-Imports only the torch/numpy functions that nothing else pins (the survey's list): receiver_chunk_mace.System
+Imports only the torch/numpy functions that nothing else pins: receiver_chunk_mace.System
 (wrap, Morton order, build_neighbors: edge order, perm tie-breaks, fp64 boundary cases) and
 mliap_threepass.ThreePassMLIAP._topology_all (local index assignment).  Nothing from the reference is copied:
 the .npz files hold inputs and outputs only.

@@ -1,6 +1,6 @@
 """GPU parity of the HIP path against the CPU oracle (marked gpu; run on the MI355X box).
 
-Tolerances: the BASELINE bar (energy 1e-5 eV/atom, forces 1e-3 eV/A max-abs) and, because the random-init model's
+Tolerances: the parity bar (energy 1e-5 eV/atom, forces 1e-3 eV/A max-abs) and, because the random-init model's
 outputs are small (|F| ~ 0.03 eV/A), also relative bars: forces within 1e-4 of max|F| against the exact fp64
 oracle (fp32 arithmetic + 512-knot tables, the reference's production numerics) and within 2e-5 against the fp64
 oracle that uses the same tables (fp32 rounding only).  Integer outputs (neighbour lists) are bit-exact.
@@ -78,7 +78,7 @@ def test_neighbor_list_large_box_matches_oracle(dev):
 
 @pytest.mark.parametrize("case", ["water98304", "fcc500000"])
 def test_neighbor_list_full_size_matches_c_oracle(dev, case):
-    """Bit-exact at BASELINE sizes: config 3's 98,304-atom water box and config 4's 500,000-atom FCC alloy
+    """Bit-exact at benchmark sizes: config 3's 98,304-atom water box and config 4's 500,000-atom FCC alloy
     (GPU cell list vs the plain-C restatement of the reference's build)."""
     from mace_onegpu import systems
     from mace_onegpu.receiver_chunk_mace import System
