@@ -18,7 +18,10 @@ Objects beside the contract fields:
   roofline     : the dominant kernel, algorithmic bytes per launch / mean launch time measured with HIP events on the
                  launch stream during the timed steps, against 8 TB/s HBM; traffic = measured HBM bytes per launch
                  from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload (or null)
-  step_roofline: atom-steps/s against the fp32 MFMA ceiling of the exact model's work per atom-step
+  node_kernels : the linears (MFMA) and the symmetric contractions (HBM roof) timed with HIP events in one extra
+                 step after the timed ones, with algorithmic bytes and FLOPs
+  step_roofline: atom-steps/s against the fp32 MFMA ceiling of the exact model's work per atom-step (edge terms,
+                 node linears and the symmetric contractions S1 / S2 per node)
   cpu_baseline : the fp64 CPU oracle (oracle/mace_ref.py, a restatement of the reference's three-pass algorithm) on a
                  bounded sample of the same workload, in the metric's unit
 """
@@ -109,14 +112,55 @@ def measured_traffic(kernel, workload):
     return rec["traffic_bytes_per_launch"]
 
 
+def node_algorithmic(name, units, symc_flops):
+    """Algorithmic HBM bytes and FLOPs of one node-level launch.
+    linear (mm_linear, MFMA): units (rows, sum of K-chunks, distinct input blocks, output components, accumulate,
+      distinct 128 x 128 weight blocks): 2 * 128 * 128 flops per row and K-chunk; each input block and output
+      component read / written once per row (accumulating outputs read too), each weight block once.
+    symc<L>_<dir>: units (rows,): symc_flops[(L, dir)] flops per row (the dense-coefficient count of the model's
+      contraction, backward = 2 x forward); bytes: the 16-component input, the output (layer 1: 4 components,
+      layer 2: 1), the backward's cotangent in and gradient out, the species index and density terms."""
+    if name == "linear":
+        rows, k_sum, n_in, n_comp, acc, n_w = units
+        return 4 * C * rows * (n_in + n_comp * (1 + acc)) + 4 * C * C * n_w, 2 * C * C * rows * k_sum
+    layer, direction = int(name[4]), name[6:]
+    (rows,) = units
+    n_out = 4 if layer == 1 else 1
+    F = rows * symc_flops[(layer, direction)]
+    if direction == "fwd":
+        return 4 * C * rows * (16 + n_out) + 4 * rows, F
+    return 4 * C * rows * (16 + n_out + 16) + 12 * rows, F
+
+
+def symc_flops_per_row(tables):
+    """{(layer, 'fwd' | 'bwd'): flops per node} of the two symmetric contractions (S1, S2 forward; 2x backward)."""
+    from mace_onegpu import codegen
+    S1 = codegen.symc_model_flops(tables.sc1, [0, 1])
+    S2 = codegen.symc_model_flops(tables.sc2, [0])
+    return {(1, "fwd"): S1, (1, "bwd"): 2 * S1, (2, "fwd"): S2, (2, "bwd"): 2 * S2}
+
+
+def node_kernel_table(fl, ktimes, steps):
+    """Per-kernel statistics of the linears and symmetric contractions (HIP-event times of one timed step)."""
+    sf = symc_flops_per_row(fl.tables)
+    out = {}
+    for name, d in ktimes.items():
+        if not (name == "linear" or name.startswith("symc")):
+            continue
+        B = sum(node_algorithmic(name, u, sf)[0] for u in d["units"])
+        F = sum(node_algorithmic(name, u, sf)[1] for u in d["units"])
+        out[name] = summarize(name, d["launches"], d["ms_total"], B, F, steps)
+    return out
+
+
 def summarize(name, launches, ms_total, B, F, steps):
     sec = ms_total * 1e-3
     k = dict(launches=launches, ms_per_launch=ms_total / launches, ms_per_step=ms_total / steps,
              GBps=B / sec / 1e9, TFLOPs=F / sec / 1e12, hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS,
              bytes_per_launch=B / launches, flops_per_launch=F / launches)
-    if name.startswith("ace1"):          # the edge products run on MFMA
+    if name.startswith(("ace1", "linear")):          # run on MFMA
         k["mfma_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
-    else:
+    elif not name.startswith("symc"):    # the contractions' count is a convention above the executed work: HBM roof
         k["valu_frac"] = F / sec / 1e12 / VALU_F32_PEAK_TFLOPS
     return k
 
@@ -172,12 +216,15 @@ def step_roofline(value, pairs_per_atom, tables):
     edge = pairs_per_atom * 2 * C * ((n1 + 4 * w1) * 2 + (2 * n1 + 8 * w1) + (n2 + 4 * w2) + (3 * n2 + 8 * w2))
     l1node = 2 * C * C * (16 + 16 + 4)
     l2node = 2 * C * C * (40 + 4 * 1.83 + 1 + 1)
-    f_atom = edge + 4 * l1node + 3 * l2node
+    sf = symc_flops_per_row(tables)
+    S1, S2 = sf[(1, "fwd")], sf[(2, "fwd")]
+    f_atom = edge + 4 * l1node + 3 * l2node + 4 * S1 + 3 * S2
     ceiling = MFMA_F32_PEAK_TFLOPS * 1e12 / f_atom
     return {"flop_per_atom_step": round(f_atom), "ceiling_atom_steps_per_s": round(ceiling), "peak_TFLOPs":
-            MFMA_F32_PEAK_TFLOPS, "frac": round(value / ceiling, 4),
-            "note": "symmetric-contraction FLOPs not counted; the evaluated algorithm does less work (layer 1 in "
-                    "the density-projection form, pass C reuses pass A's layer-1 state)"}
+            MFMA_F32_PEAK_TFLOPS, "frac": round(value / ceiling, 4), "S1_flop_per_node": S1, "S2_flop_per_node": S2,
+            "note": "S1, S2: forward symmetric-contraction FLOPs per node, 2 (nu + 1) per non-zero of each path's "
+                    "coupling tensor and channel (backward 2x forward); the evaluated algorithm does less work (layer "
+                    "1 in the density-projection form, pass C reuses pass A's layer-1 state, factorised contractions)"}
 
 
 def ncores():
@@ -283,13 +330,16 @@ def copy_calibration(mib):
     torch.cuda.synchronize()
 
 
+def rounded(kernels):
+    return {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+            for k, v in kernels.items()}
+
+
 def base_line(a, metric, value, ms, unit, data, config, roof, kernels, cpu, higher=True):
     return {"metric": metric, "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": a.steps,
             "warmup": a.warmup, "ms_per_step": round(ms, 3), "higher_is_better": higher, "scaling": "weak",
             "vs_baseline": None, "dtype": "fp32", "data": data, "config": config, "roofline": roof,
-            "kernels": {k: {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                        for k, v in kernels.items()},
-            "cpu_baseline": cpu}
+            "kernels": rounded(kernels), "cpu_baseline": cpu}
 
 
 # ----------------------------------------------------------------------------- config 5: MD
@@ -321,9 +371,13 @@ def run_md(a):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
+    n_pairs = int(md.pairs.E)
+    # one more step, after the timed ones, with the linears' and contractions' launches timed as well
+    fl.start_kernel_timing(node_kernels=True)
+    md.step()
+    nodes = node_kernel_table(fl, fl.stop_kernel_timing(), 1)
     if a.copy_calib_mib > 0:
         copy_calibration(a.copy_calib_mib)
-    n_pairs = int(md.pairs.E)
     value = N * a.steps / dt
     kernels = kernel_table(fl, ktimes, a.steps)
     roof = roofline_of(kernels, {"n_mol": a.n_mol, "chunk": a.chunk})
@@ -336,6 +390,7 @@ def run_md(a):
                       "rebuilds_timed": md.n_rebuild - rebuilds0,
                       "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2),
                       "box_A": round(float(box[0]), 4)}, roof, kernels, cpu)
+    line["node_kernels"] = rounded(nodes)
     line["step_roofline"] = step_roofline(value, n_pairs / N, fl.tables)
     return line
 
@@ -380,6 +435,11 @@ def run_ef(a):
     ktimes = fl.stop_kernel_timing()
     value = s.N * a.steps / dt
     kernels = kernel_table(fl, ktimes, a.steps) if not graphs else {}
+    nodes = {}
+    if not graphs:      # one more evaluation with the linears' and contractions' launches timed as well
+        fl.start_kernel_timing(node_kernels=True)
+        ev.compute(s)
+        nodes = node_kernel_table(fl, fl.stop_kernel_timing(), 1)
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline_water() if a.config == 3 else cpu_baseline_fcc()
@@ -392,6 +452,8 @@ def run_ef(a):
                      roofline_of(kernels), kernels, cpu)
     if graphs:
         line["roofline_note"] = "per-kernel HIP-event timing is not available inside graph replays (rocprofv3)"
+    else:
+        line["node_kernels"] = rounded(nodes)
     line["step_roofline"] = step_roofline(value, n_pairs / s.N, fl.tables)
     return line
 

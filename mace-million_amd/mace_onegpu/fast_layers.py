@@ -27,6 +27,7 @@ from ._lib import K, stream
 C = 128
 NCB = 8
 SRC = 3                         # max K-chunks of one linear output component (mm_linear)
+NODE_KERNELS = ("linear", "symc1_fwd", "symc1_bwd", "symc2_fwd", "symc2_bwd")
 ACE_H = 64                      # hidden features of the layer-1 ACE kernels (csrc/ace.hip)
 ACE_MAX_S = 4                   # species per system of the layer-1 ACE kernels
 
@@ -61,6 +62,10 @@ class LinPlan:
             outoff.append(out_off)
         self.nsrc, self.inoff = host_ints(nsrc), host_ints(inoff)
         self.widx, self.outoff = host_ints(widx), host_ints(outoff)
+        # work of one launch per row: 128 x 128 products, distinct input blocks read, distinct weight blocks
+        self.k_sum = sum(nsrc)
+        self.n_in = len({io for _, srcs in comps for io, _ in srcs})
+        self.n_w = len({wi for _, srcs in comps for _, wi in srcs})
 
 
 def comp_of(ls):
@@ -164,10 +169,14 @@ class FastLayers:
         self.nO1, self.nO2 = self.tables.tp1["nO"], self.tables.tp2["nO"]
         self.ws = None
         self.ktimer = None        # list of (name, units, start event, end event) while kernel timing is on
+        self.ktimer_nodes = False
 
     # ------------------------------------------------------------------ per-launch timing (HIP events)
-    def start_kernel_timing(self):
+    def start_kernel_timing(self, node_kernels=False):
+        """Time the edge kernels' launches with HIP events; node_kernels=True also times the linears and the
+        symmetric contractions (many short launches: their events are kept out of a headline timing)."""
         self.ktimer = []
+        self.ktimer_nodes = node_kernels
 
     def stop_kernel_timing(self):
         """{name: dict(launches, ms_total, units)} of the timed launches; synchronises."""
@@ -182,7 +191,7 @@ class FastLayers:
         return out
 
     def _timed(self, name, units, fn, *args):
-        if self.ktimer is None:
+        if self.ktimer is None or (name in NODE_KERNELS and not self.ktimer_nodes):
             return fn(*args)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -292,13 +301,15 @@ class FastLayers:
     def _lin(self, plan, inp, in_stride, out, out_stride, W, rows, in_rows=None, out_rows=None, scale=None,
              scale_mode=0, species=False, accumulate=0, w_group_stride=0):
         ws = self.ws
+        units = (rows, plan.k_sum, plan.n_in, plan.n, accumulate, plan.n_w * (self.S if species else 1))
         if species:
-            K.mm_linear(inp, in_stride, in_rows, out, out_stride, out_rows, W, scale, scale_mode, ws["lists"],
-                        ws["counts"], ws["lists_stride"], self.S, w_group_stride, rows, accumulate, plan.n, plan.nsrc,
-                        plan.inoff, plan.widx, plan.outoff, stream())
+            self._timed("linear", units, K.mm_linear, inp, in_stride, in_rows, out, out_stride, out_rows, W, scale,
+                        scale_mode, ws["lists"], ws["counts"], ws["lists_stride"], self.S, w_group_stride, rows,
+                        accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, stream())
         else:
-            K.mm_linear(inp, in_stride, in_rows, out, out_stride, out_rows, W, scale, scale_mode, None, None, 0, 1, 0,
-                        rows, accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, stream())
+            self._timed("linear", units, K.mm_linear, inp, in_stride, in_rows, out, out_stride, out_rows, W, scale,
+                        scale_mode, None, None, 0, 1, 0, rows, accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx,
+                        plan.outoff, stream())
 
     def _geometry(self, k, g):
         """Edge geometry of chunk g for interaction block k (LAMMPS pair vectors or positions)."""
@@ -348,7 +359,8 @@ class FastLayers:
                         ws["e_u"], self.Xs1, C, self.tab[0], self.n_tab, self.M, ws["A"], rho_out, stream())
             self._lin(self.plan_l1, ws["A"], 16 * C, M_out, 16 * C, self.W_l1, g.nC, scale=rho_out, scale_mode=1,
                       species=True, w_group_stride=4)
-        K.mm_symc1_fwd(g.nC, M_out, 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C, stream())
+        self._timed("symc1_fwd", (g.nC,), K.mm_symc1_fwd, g.nC, M_out, 16 * C, ws["spec"], self.Wsc1, ws["B"], 4 * C,
+                    stream())
         self._lin(self.plan_p1, ws["B"], 4 * C, h1_out, 4 * C, self.W_p1, g.nC)
 
     def pass_a(self, g, H1, cache=None):
@@ -375,8 +387,8 @@ class FastLayers:
         K.mm_readout1(g.nC, h1, D1, self.r0s, self.scale, eat[g.a:g.b], G1r[g.a:g.b], D1, ws["gh"], D1, D1,
                       stream())
         self._lin(self.plan_p1, ws["gh"], D1, ws["gB"], D1, self.W_p1T, g.nC)
-        K.mm_symc1_bwd(g.nC, Mc, 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1, ws["gM"], 16 * C, rho, ws["g_rho"],
-                       stream())
+        self._timed("symc1_bwd", (g.nC,), K.mm_symc1_bwd, g.nC, Mc, 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1,
+                    ws["gM"], 16 * C, rho, ws["g_rho"], stream())
         if self.ace:
             Kp = self.ace_Kp
             self._lin(self.plan_aceT, ws["gM"], 16 * C, ws["gA"], 16 * Kp, self.W_aceT, g.nC, scale=rho,
@@ -410,14 +422,15 @@ class FastLayers:
                     ws["Xh"], D1, self.tab[1], self.n_tab, self.M, ws["A"], ws["rho"], stream())
         self._lin(self.plan_lin2, ws["A"], self.nO2 * C, ws["M"], 16 * C, self.W_lin2, g.nC, scale=ws["rho"],
                   scale_mode=1)
-        K.mm_symc2_fwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, B2, C, stream())
+        self._timed("symc2_fwd", (g.nC,), K.mm_symc2_fwd, g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, B2, C,
+                    stream())
         self._lin(self.plan_p2, B2, C, h2, C, self.W_p2, g.nC, accumulate=1)
         K.mm_readout2(g.nC, h2, C, self.r1W1, self.r1w2, self.H_ro, mm.SILU_NORM, self.scale, eat[g.a:g.b], gh2, C,
                       stream())
         # ---- backward
         self._lin(self.plan_p2, gh2, C, gB2, C, self.W_p2T, g.nC)
-        K.mm_symc2_bwd(g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, gB2, C, ws["gM"], 16 * C, ws["rho"],
-                       ws["g_rho"], stream())
+        self._timed("symc2_bwd", (g.nC,), K.mm_symc2_bwd, g.nC, ws["M"], 16 * C, ws["spec"], self.Wsc2, gB2, C,
+                    ws["gM"], 16 * C, ws["rho"], ws["g_rho"], stream())
         self._lin(self.plan_lin2T, ws["gM"], 16 * C, ws["gA"], self.nO2 * C, self.W_lin2T, g.nC, scale=ws["rho"],
                   scale_mode=1)
         K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
