@@ -58,6 +58,15 @@ __device__ __forceinline__ float mm_row_sum16(float v) {
   return v;
 }
 
+// Orders the LDS accesses of the lanes of one wave: what a lane wrote before the call is seen by every lane's reads
+// after it.  One wave's LDS instructions execute in program order; the fences keep the compiler from moving
+// accesses across the call (no s_barrier: the lanes of other waves are not waited for).
+__device__ __forceinline__ void mm_wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Four float adds to LDS (p[0], p[16], p[32], p[48]) through 32-bit compare-and-swap, issued together; a lane
 // repeats only the adds whose swap lost a race.  The native LDS float atomic add (ds_add_f32) runs far below
 // the integer LDS atomics on this GPU (measured), so float sums shared by the waves of a workgroup use this.
