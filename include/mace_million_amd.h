@@ -152,9 +152,10 @@ int mm_symc2_bwd(int n, const float* x, long x_stride, const int* spec, const fl
                  long gout_stride, float* gx, long gx_stride, const float* rho, float* g_rho, mm_stream_t stream);
 /* Equivariant linears on MFMA: linear_up, linear (with / (rho+1)), species-block skip_tp (replaces
  * fast_layers.SpeciesSkip, fast_layers.py:41-105), product linear, and transposes.  comp_* are HOST arrays:
- * nsrc [n_comp], in_off / w_idx [n_comp][3], out_off [n_comp]. */
+ * nsrc [n_comp], in_off / w_idx [n_comp][3], out_off [n_comp].  W: 128 x 128 weight blocks, each as three bf16
+ * planes W0 + W1 + W2 = W (fast_layers.mfma_block); products at fp32 accuracy, fp32 accumulation. */
 int mm_linear(const float* in, long in_stride, const int* in_rows, float* out, long out_stride, const int* out_rows,
-              const float* W, const float* row_scale, int scale_mode, const int* list, const int* list_count,
+              const void* W, const float* row_scale, int scale_mode, const int* list, const int* list_count,
               long list_stride, int n_groups, int w_group_stride, int n_rows_max, int accumulate, int n_comp,
               const int* comp_nsrc, const int* comp_in_off, const int* comp_w_idx, const int* comp_out_off,
               mm_stream_t stream);

@@ -1,4 +1,5 @@
-// Equivariant linear maps of the node features on the fp32 matrix cores (v_mfma_f32_16x16x4f32).
+// Equivariant linear maps of the node features on the matrix cores, at fp32 accuracy from bf16 products
+// (v_mfma_f32_16x16x32_bf16, fp32 accumulation).
 //
 // Every node-level linear of the two layers is a set of 128x128 channel-mixing blocks applied to 128-channel rows
 // of ir_mul features (one row per (node, component)): linear_up, linear (with the density division), skip_tp per
@@ -6,26 +7,34 @@
 // row lists instead of computing every species and selecting), the product-block linear, and their transposes in
 // the backward passes.  For each output component j of one launch:
 //     out[out_row(r), comp_j] (= or +=) scale(r) * sum_q in[in_row(r), src_{j,q}] @ W[w_{j,q}]
-// Launch: grid (ceil(rows / (128 n_blk)), n_comp, n_groups); 512 threads = 8 waves, each wave 16 rows x 128
-// columns (8 MFMA tiles) of each of its n_blk row blocks; the 128x128 weight block is staged in LDS (64 KiB) in the
-// lane order of the B operand.
-// Weight blocks are stored pre-permuted: element W[k][n], k = 16 t + 4 g + u, n = 16 nt + i, at float index
-// (((t * 8 + nt) * 4 + g) * 16 + i) * 4 + u, so that lane (i, g) reads its 4 k-values of step t and tile nt as one
-// 16-byte LDS read, the 16 lanes of a group reading 256 consecutive bytes (no bank conflicts), and the A operand of
-// lane (row, g) is the float4 in[row][16 t + 4 g .. + 3].
+//
+// Split products.  Every fp32 operand is the sum of three bf16 values, x = x0 + x1 + x2 with x0 = bf16(x),
+// x1 = bf16(x - x0), x2 = bf16(x - x0 - x1) (round to nearest even; the differences are exact in fp32), so that
+// |x - x0 - x1 - x2| <= 2^-27 |x|.  A product a b is taken as the six bf16 products a_i b_j with i + j <= 2; the
+// omitted ones are below 3 * 2^-24 |a b|, the size of an fp32 rounding, and every sum is accumulated in fp32.
+// Six 16x16x32 bf16 products take 96 cycles against 256 for the same K = 32 in v_mfma_f32_16x16x4f32.  The
+// weights are split once on the host; the input rows are split as they are loaded.
+//
+// Launch: grid (ceil(rows / (256 n_blk)), n_comp, n_groups); 1024 threads = 16 waves, each wave 16 rows x 128
+// columns (8 MFMA tiles) of each of its n_blk row blocks; the weight block (3 bf16 planes of 128 x 128, 96 KiB)
+// is staged in LDS in the lane order of the B operand.  16 waves of one workgroup per CU = 4 waves per SIMD.
+// Weight blocks: plane p of block b at bf16 offset (3 b + p) 16384; element W[k][n], k = 32 t + 8 g + u,
+// n = 16 nt + i, at (((t * 8 + nt) * 4 + g) * 16 + i) * 8 + u, so that lane (i, g) reads its 8 k-values of step t
+// and tile nt as one 16-byte LDS read, the 16 lanes of a group reading 256 consecutive bytes (no bank conflicts);
+// the A operand of lane (row, g) is in[row][32 t + 8 g .. + 7].
 #include "common.h"
 
 #include <algorithm>
 
 #define MM_LIN_MAX_COMP 48
 #define MM_LIN_MAX_SRC 3
-// 8 waves of one 16-row M-tile each: 128 rows per workgroup block.  With the 64 KiB weight block in LDS two
-// workgroups share a CU, i.e. 4 waves per SIMD (measured faster than 4 waves of two M-tiles, 2 waves per SIMD).
-#define MM_LIN_MT 1
-#define MM_LIN_NW 8
-#define MM_LIN_BLOCK_ROWS (16 * MM_LIN_MT * MM_LIN_NW)
-// a launch keeps at least this many workgroups (8 per CU) when it groups row blocks per workgroup
-#define MM_LIN_MIN_WG 2048
+#define MM_LIN_NW 16
+#define MM_LIN_BLOCK_ROWS (16 * MM_LIN_NW)
+// a launch keeps at least this many workgroups (4 per CU) when it groups row blocks per workgroup
+#define MM_LIN_MIN_WG 1024
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx8 __attribute__((ext_vector_type(8)));
 
 struct MMLinComp {
   int n_src;
@@ -41,7 +50,7 @@ struct MMLinArgs {
   float* out;
   long out_stride;
   const int* out_rows;    // nullable
-  const float* W;         // weight blocks, 16384 floats each
+  const uint4* W;         // weight blocks: 3 bf16 planes of 16384 values each (6144 x 16 B per block)
   const float* row_scale; // nullable: per logical row id
   int scale_mode;         // 0: scale = row_scale[id]; 1: scale = 1 / (row_scale[id] + 1)
   const int* list;        // nullable: per group g, list[g * list_stride + r] = logical row id
@@ -54,132 +63,117 @@ struct MMLinArgs {
   MMLinComp comp[MM_LIN_MAX_COMP];
 };
 
-template <int MT>
 struct MMLinRows {
-  bool valid[MT];
-  long in_row[MT];
+  bool valid;
+  long in_row;
 };
 
-template <int MT>
 __device__ __forceinline__ void mm_lin_rows(const MMLinArgs& args, const int* list, int nrows, int row0, int wave,
-                                            int i, MMLinRows<MT>& rw) {
+                                            int i, MMLinRows& rw) {
+  const int r = row0 + wave * 16 + i;
+  rw.valid = r < nrows;
+  const int rid = rw.valid ? (list ? list[r] : r) : 0;
+  rw.in_row = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
+}
+
+// A operands of one source: lane (i, g) holds in[row i][32 t + 8 g .. + 7] in a[2 t], a[2 t + 1] (t = 0..3)
+__device__ __forceinline__ void mm_lin_load_a(const MMLinArgs& args, const MMLinRows& rw, int in_off, int g,
+                                              floatx4 (&a)[8]) {
+  const float* __restrict__ ap = args.in + rw.in_row * args.in_stride + in_off + 8 * g;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int r = row0 + (wave * MT + mt) * 16 + i;
-    rw.valid[mt] = r < nrows;
-    const int rid = rw.valid[mt] ? (list ? list[r] : r) : 0;
-    rw.in_row[mt] = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
+  for (int t = 0; t < 4; ++t) {
+    a[2 * t] = rw.valid ? *(const floatx4*)(ap + 32 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
+    a[2 * t + 1] = rw.valid ? *(const floatx4*)(ap + 32 * t + 4) : floatx4{0.f, 0.f, 0.f, 0.f};
   }
 }
 
-template <int MT>
-__device__ __forceinline__ void mm_lin_load_a(const MMLinArgs& args, const MMLinRows<MT>& rw, int in_off, int g,
-                                              floatx4 (&a)[MT][8]) {
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const float* __restrict__ ap = args.in + rw.in_row[mt] * args.in_stride + in_off + 4 * g;
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-      a[mt][t] = rw.valid[mt] ? *(const floatx4*)(ap + 16 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
-  }
+// x = x0 + x1 + x2 (bf16, round to nearest even; both differences are exact in fp32)
+__device__ __forceinline__ void mm_split3_bf16(const floatx8& x, bf16x8& x0, bf16x8& x1, bf16x8& x2) {
+  x0 = __builtin_convertvector(x, bf16x8);
+  const floatx8 r1 = x - __builtin_convertvector(x0, floatx8);
+  x1 = __builtin_convertvector(r1, bf16x8);
+  const floatx8 r2 = r1 - __builtin_convertvector(x1, floatx8);
+  x2 = __builtin_convertvector(r2, bf16x8);
 }
 
-// MT = 16-row M-tiles per wave, NW waves (rows per workgroup block = 16 NW MT): every B operand read from LDS
-// feeds MT MFMAs.
 // A workgroup handles n_blk consecutive row blocks of one output component; with a single source the weight block
-// is staged in LDS once for all of them.  The A operands of the next (block, source) step are loaded while the
-// MFMAs of the current one run.
-template <int MT, int NW>
-__global__ void __launch_bounds__(64 * NW) mm_linear_kernel(MMLinArgs args, int n_blk) {
-  __shared__ floatx4 Wl[4096];
-  const MMLinComp cp = args.comp[blockIdx.y];
+// is staged in LDS once for all of them.
+__global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs args, int n_blk) {
+  __shared__ uint4 Wl[3 * 2048];
+  const MMLinComp& cp = args.comp[blockIdx.y];   // kernel-argument memory, read with uniform indices
   const int grp = blockIdx.z;
   const int nrows = args.list ? args.list_count[grp] : args.n_rows;
-  const int blk_rows = 16 * NW * MT;
   const int blk0 = blockIdx.x * n_blk;
-  if (blk0 * blk_rows >= nrows) return;
-  const int blk1 = min(blk0 + n_blk, (nrows + blk_rows - 1) / blk_rows);
+  if (blk0 * MM_LIN_BLOCK_ROWS >= nrows) return;
+  const int blk1 = min(blk0 + n_blk, (nrows + MM_LIN_BLOCK_ROWS - 1) / MM_LIN_BLOCK_ROWS);
   const int* __restrict__ list = args.list ? args.list + (size_t)grp * args.list_stride : nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
   const int n_src = cp.n_src;
   const bool restage = n_src > 1;
-  MMLinRows<MT> rw, rw_next;
-  mm_lin_rows<MT>(args, list, nrows, blk0 * blk_rows, wave, i, rw);
-  floatx4 a[MT][8];
-  mm_lin_load_a<MT>(args, rw, cp.in_off[0], g, a);
+  MMLinRows rw;
+  mm_lin_rows(args, list, nrows, blk0 * MM_LIN_BLOCK_ROWS, wave, i, rw);
   for (int blk = blk0; blk < blk1; ++blk) {
-    const int row0 = blk * blk_rows;
-    floatx4 acc[MT][8];
+    const int row0 = blk * MM_LIN_BLOCK_ROWS;
+    floatx4 acc[8];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) acc[mt][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < 8; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int q = 0; q < n_src; ++q) {
-      // next step: source q + 1 of this block, else source 0 of the next block
-      floatx4 an[MT][8];
-      const bool next_here = q + 1 < n_src;
-      const bool has_next = next_here || blk + 1 < blk1;
-      if (has_next) {
-        if (!next_here) mm_lin_rows<MT>(args, list, nrows, row0 + blk_rows, wave, i, rw_next);
-        mm_lin_load_a<MT>(args, next_here ? rw : rw_next, cp.in_off[next_here ? q + 1 : 0], g, an);
-      }
+      floatx4 a[8];
+      mm_lin_load_a(args, rw, cp.in_off[q], g, a);
       if (restage || blk == blk0) {
-        const floatx4* __restrict__ Wg =
-            (const floatx4*)(args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 16384);
+        const uint4* __restrict__ Wg = args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 6144;
         __syncthreads();
-        for (int j = threadIdx.x; j < 4096; j += 64 * NW) Wl[j] = Wg[j];
+        for (int j = threadIdx.x; j < 6144; j += 64 * MM_LIN_NW) Wl[j] = Wg[j];
         __syncthreads();
       }
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
+      for (int t = 0; t < 4; ++t) {
+        const floatx8 x = {a[2 * t].x, a[2 * t].y, a[2 * t].z, a[2 * t].w,
+                           a[2 * t + 1].x, a[2 * t + 1].y, a[2 * t + 1].z, a[2 * t + 1].w};
+        bf16x8 a0, a1, a2;
+        mm_split3_bf16(x, a0, a1, a2);
 #pragma unroll
         for (int nt = 0; nt < 8; ++nt) {
-          const floatx4 b = Wl[((t * 8 + nt) * 4 + g) * 16 + i];
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt) {
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].x, b.x, acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].y, b.y, acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].z, b.z, acc[mt][nt], 0, 0, 0);
-            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[mt][t].w, b.w, acc[mt][nt], 0, 0, 0);
-          }
+          const int o = ((t * 8 + nt) * 4 + g) * 16 + i;
+          const bf16x8 b0 = __builtin_bit_cast(bf16x8, Wl[o]);
+          const bf16x8 b1 = __builtin_bit_cast(bf16x8, Wl[2048 + o]);
+          const bf16x8 b2 = __builtin_bit_cast(bf16x8, Wl[4096 + o]);
+          // smallest terms first
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b0, acc[nt], 0, 0, 0);
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b2, acc[nt], 0, 0, 0);
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[nt], 0, 0, 0);
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b0, acc[nt], 0, 0, 0);
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b1, acc[nt], 0, 0, 0);
+          acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[nt], 0, 0, 0);
         }
-      }
-      if (has_next) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int t = 0; t < 8; ++t) a[mt][t] = an[mt][t];
       }
     }
     // D layout of the 16x16 tile: lane (i, g) holds rows 4 g + v (v = 0..3) of column i
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int v = 0; v < 4; ++v) {
+      const int rr = row0 + wave * 16 + 4 * g + v;
+      if (rr >= nrows) continue;
+      const int id = list ? list[rr] : rr;
+      const long orow = args.out_rows ? (long)args.out_rows[id] : (long)id;
+      float s = 1.f;
+      if (args.row_scale) s = args.scale_mode == 1 ? 1.f / (args.row_scale[id] + 1.f) : args.row_scale[id];
+      float* __restrict__ op = args.out + orow * args.out_stride + cp.out_off + i;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int rr = row0 + (wave * MT + mt) * 16 + 4 * g + v;
-        if (rr >= nrows) continue;
-        const int id = list ? list[rr] : rr;
-        const long orow = args.out_rows ? (long)args.out_rows[id] : (long)id;
-        float s = 1.f;
-        if (args.row_scale) s = args.scale_mode == 1 ? 1.f / (args.row_scale[id] + 1.f) : args.row_scale[id];
-        float* __restrict__ op = args.out + orow * args.out_stride + cp.out_off + i;
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          const float val = s * acc[mt][nt][v];
-          if (args.accumulate)
-            op[16 * nt] += val;
-          else
-            op[16 * nt] = val;
-        }
+      for (int nt = 0; nt < 8; ++nt) {
+        const float val = s * acc[nt][v];
+        if (args.accumulate)
+          op[16 * nt] += val;
+        else
+          op[16 * nt] = val;
       }
     }
-    rw = rw_next;
+    if (blk + 1 < blk1) mm_lin_rows(args, list, nrows, row0 + MM_LIN_BLOCK_ROWS, wave, i, rw);
   }
 }
 
 // Flat argument form for the C ABI: comp table as int arrays [n_comp][MM_LIN_MAX_SRC] etc.
 extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, float* out, long out_stride,
-                         const int* out_rows, const float* W, const float* row_scale, int scale_mode,
+                         const int* out_rows, const void* W, const float* row_scale, int scale_mode,
                          const int* list, const int* list_count, long list_stride, int n_groups, int w_group_stride,
                          int n_rows_max, int accumulate, int n_comp, const int* comp_nsrc, const int* comp_in_off,
                          const int* comp_w_idx, const int* comp_out_off, hipStream_t stream) {
@@ -195,7 +189,7 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
   a.out = out;
   a.out_stride = out_stride;
   a.out_rows = out_rows;
-  a.W = W;
+  a.W = (const uint4*)W;
   a.row_scale = row_scale;
   a.scale_mode = scale_mode;
   a.list = list;
@@ -221,6 +215,6 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
   const long per_blk = (long)n_comp * n_groups;
   const int n_blk = (int)std::max(1L, std::min(8L, n_blocks * per_blk / MM_LIN_MIN_WG));
   dim3 grid((unsigned)((n_blocks + n_blk - 1) / n_blk), n_comp, n_groups);
-  hipLaunchKernelGGL((mm_linear_kernel<MM_LIN_MT, MM_LIN_NW>), grid, dim3(64 * MM_LIN_NW), 0, stream, a, n_blk);
+  hipLaunchKernelGGL(mm_linear_kernel, grid, dim3(64 * MM_LIN_NW), 0, stream, a, n_blk);
   return mm::launch_status("mm_linear");
 }

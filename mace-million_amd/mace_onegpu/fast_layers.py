@@ -32,12 +32,24 @@ ACE_H = 64                      # hidden features of the layer-1 ACE kernels (cs
 ACE_MAX_S = 4                   # species per system of the layer-1 ACE kernels
 
 
+def split3_bf16(W):
+    """fp32 W -> (W0, W1, W2) bf16 with W0 = bf16(W), W1 = bf16(W - W0), W2 = bf16(W - W0 - W1) (round to nearest
+    even; the differences are exact in fp32): |W - W0 - W1 - W2| <= 2^-27 |W|."""
+    W = W.to(torch.float32)
+    w0 = W.to(torch.bfloat16)
+    r1 = W - w0.float()
+    w1 = r1.to(torch.bfloat16)
+    w2 = (r1 - w1.float()).to(torch.bfloat16)
+    return w0, w1, w2
+
+
 def mfma_block(W):
-    """[128, 128] (k, n) -> flat float32 in the LDS order of mm_linear's B operand: W[k][n] with k = 16 t + 4 g + u,
-    n = 16 nt + i at float index (((t * 8 + nt) * 4 + g) * 16 + i) * 4 + u, so that the 16 lanes (i, g) of one
-    16-byte LDS read take 256 consecutive bytes (no bank conflicts)."""
-    W = W.reshape(8, 4, 4, 8, 16)             # [t, g, u, nt, i]
-    return W.permute(0, 3, 1, 4, 2).reshape(-1).contiguous()
+    """[128, 128] (k, n) -> flat bf16 [3 * 16384]: the three planes of split3_bf16(W), each in the LDS order of
+    mm_linear's B operand: W[k][n] with k = 32 t + 8 g + u, n = 16 nt + i at (((t * 8 + nt) * 4 + g) * 16 + i) * 8
+    + u, so that the 16 lanes (i, g) of one 16-byte LDS read take 256 consecutive bytes (no bank conflicts)."""
+    def order(P):
+        return P.reshape(4, 4, 8, 8, 16).permute(0, 3, 1, 4, 2).reshape(-1)   # [t, g, u, nt, i] -> [t, nt, g, i, u]
+    return torch.cat([order(p) for p in split3_bf16(W.reshape(128, 128))]).contiguous()
 
 
 def host_ints(vals):
