@@ -18,8 +18,9 @@ Objects beside the contract fields:
   roofline     : the dominant kernel, algorithmic bytes per launch / mean launch time measured with HIP events on the
                  launch stream during the timed steps, against 8 TB/s HBM; traffic = measured HBM bytes per launch
                  from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload (or null)
-  node_kernels : the linears (MFMA) and the symmetric contractions (HBM roof) timed with HIP events in one extra
-                 step after the timed ones, with algorithmic bytes and FLOPs
+  node_kernels : the linears (bf16 MFMA: mfma_frac = 6 F / t / 2.5 PFLOP/s; fp32_equiv_frac = F / t / 157.3) and the
+                 symmetric contractions (HBM roof) timed with HIP events in one extra step after the timed ones, with
+                 algorithmic bytes and FLOPs
   step_roofline: atom-steps/s against the fp32 MFMA ceiling of the exact model's work per atom-step (edge terms,
                  node linears and the symmetric contractions S1 / S2 per node)
   cpu_baseline : the fp64 CPU oracle (oracle/mace_ref.py, a restatement of the reference's three-pass algorithm) on a
@@ -37,6 +38,7 @@ sys.path.insert(0, os.path.join(ROOT, "mace-million_amd"))
 HBM_PEAK_GBS = 8000.0
 VALU_F32_PEAK_TFLOPS = 78.6      # fp32 vector FMA without packed-FP32 instructions (the build disables them)
 MFMA_F32_PEAK_TFLOPS = 157.3
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA (the linears: fp32 products as six bf16 products)
 C = 128
 
 
@@ -158,8 +160,11 @@ def summarize(name, launches, ms_total, B, F, steps):
     k = dict(launches=launches, ms_per_launch=ms_total / launches, ms_per_step=ms_total / steps,
              GBps=B / sec / 1e9, TFLOPs=F / sec / 1e12, hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS,
              bytes_per_launch=B / launches, flops_per_launch=F / launches)
-    if name.startswith(("ace1", "linear")):          # run on MFMA
+    if name.startswith("ace1"):          # fp32 MFMA
         k["mfma_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
+    elif name == "linear":               # six bf16 MFMA products per fp32 product
+        k["mfma_frac"] = 6 * F / sec / 1e12 / MFMA_BF16_PEAK_TFLOPS
+        k["fp32_equiv_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
     elif not name.startswith("symc"):    # the contractions' count is a convention above the executed work: HBM roof
         k["valu_frac"] = F / sec / 1e12 / VALU_F32_PEAK_TFLOPS
     return k
