@@ -236,7 +236,7 @@ def ncores():
     return len(os.sched_getaffinity(0))
 
 
-def cpu_baseline_water(n_mol=512, seed=0):
+def cpu_baseline_water(n_mol=1024, seed=0):
     """fp64 CPU oracle, one full E+F of a water box from the same generator."""
     import numpy as np
     import torch
