@@ -45,16 +45,17 @@ C = 128
 def conv_algorithmic(name, E, nC, N, tab, Kp=128):
     """Algorithmic HBM bytes and FLOPs of one convolution launch (per-edge, per-receiver and per-node terms;
     tables read once).  P = distinct tables (1: this model's radial weights do not depend on the species).
-    ace1_*: layer 1 in the density-projection form -- per edge the 16 B record and 16 harmonics (fwd; bwd also
-    writes 17 floats), the 64-feature table once, B / gB [nC, 16, Kp] once; FLOPs = the 64 x 16 outer product
-    (fwd) or its two transposed products (bwd) plus the spline evaluation.
+    ace1_*: layer 1 in the density-projection form -- per edge the 16 B record and the 16 B edge vector (the
+    harmonics are evaluated in the kernel; bwd also writes 17 floats), the 64-feature table once, B / gB
+    [nC, 16, Kp] once; FLOPs = the 64 x 16 outer product (fwd) or its two transposed products (bwd) plus the
+    spline evaluation.
     tpw_*: explicit per-edge weights (FusedConvTP) -- W [E, nW, 128] and Y read once."""
     P, M = 1, 512
     if name.startswith("ace1"):
         tab_bytes = 16 * (M - 1) * 64
         if name == "ace1_fwd":
-            return 80 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp + 4 * nC, 2 * E * 64 * 16 + 6 * E * 64
-        return 148 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp, 4 * E * 64 * 16 + 10 * E * 64
+            return 32 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp + 4 * nC, 2 * E * 64 * 16 + 6 * E * 64
+        return 100 * E + 4 * (nC + 1) + tab_bytes + 4 * nC * 16 * Kp, 4 * E * 64 * 16 + 10 * E * 64
     nX, nW, nO, nT = tab["nX"], tab["nW"], tab["nO"], len(tab["terms"])
     if name.startswith("tpw"):
         if name.endswith("fwd"):
@@ -76,8 +77,8 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
 KERNEL_SOURCES = {
     "mm_conv2_bwd_kernel": ("gen/conv_l2.hip", "gen/sh.h", "common.h"),
     "mm_conv2_fwd_kernel": ("gen/conv_l2.hip", "gen/sh.h", "common.h"),
-    "mm_ace1_fwd_kernel": ("ace.hip", "common.h"),
-    "mm_ace1_bwd_kernel": ("ace.hip", "common.h"),
+    "mm_ace1_fwd_kernel": ("ace.hip", "gen/sh.h", "common.h"),
+    "mm_ace1_bwd_kernel": ("ace.hip", "gen/sh.h", "common.h"),
     "mm_linear_kernel": ("linear.hip", "common.h"),
     "mm_fill_f32_kernel": ("node.hip", "common.h"),
     "mm_fill_i32_kernel_nl": ("nlist.hip", "common.h"),
@@ -494,7 +495,6 @@ def run_conv(a):
     gA1 = torch.randn(nC, 16 * C, device="cuda", generator=gen2)
     fl._geometry(0, g)
     pk1, eu1 = ws["e_pk"][:E].clone(), ws["e_u"][:E].clone()
-    eY1 = ws["e_Y"][:E].clone() if fl.ace else None
     fl._geometry(1, g)
     pk2, eu2 = ws["e_pk"][:E].clone(), ws["e_u"][:E].clone()
     out1 = torch.empty(nC, 16 * C, device="cuda")
@@ -515,9 +515,9 @@ def run_conv(a):
                                              gA2, part, E * 17, gX, st), fl.tables.tp2),
     }
     if fl.ace:
-        calls["ace1_fwd"] = (lambda: K.mm_ace1_fwd(g.rowptr, nC, pk1, eY1, fl.tab_h, fl.S, fl.S_pad, Bace, rho, st),
+        calls["ace1_fwd"] = (lambda: K.mm_ace1_fwd(g.rowptr, nC, pk1, eu1, fl.tab_h, fl.S, fl.S_pad, Bace, rho, st),
                              fl.tables.tp1)
-        calls["ace1_bwd"] = (lambda: K.mm_ace1_bwd(g.rowptr, nC, pk1, eY1, fl.tab_h, fl.S, fl.S_pad, gM1, fl.inv_h,
+        calls["ace1_bwd"] = (lambda: K.mm_ace1_bwd(g.rowptr, nC, pk1, eu1, fl.tab_h, fl.S, fl.S_pad, gM1, fl.inv_h,
                                                    part, st), fl.tables.tp1)
     # explicit-weight FusedConvTP kernels (V1, V2 and the literal V3 table 0e+1o+2e+3o) on the same edges
     Y16 = torch.from_numpy(o3.spherical_harmonics(g.rij.cpu().numpy())).float().cuda()

@@ -24,6 +24,7 @@ typedef void* mm_stream_t; /* hipStream_t */
 
 /* ---------------------------------------------------------------------------------------------- library */
 const char* mm_last_error(void);
+/* version of the argument conventions (3); a host binding must refuse a library of another version */
 int mm_version(void);
 /* channel count (128), channel blocks (8, one per XCD) and channels per block (16) the kernels were built for */
 int mm_build_info(int* channels, int* channel_blocks, int* block_channels);
@@ -102,10 +103,11 @@ int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u,
  * densities; the 64 -> 128-channel map, linear and skip_tp are applied by mm_linear with folded weights.
  * Backward from gB = dL/dB: part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m (one partial, for mm_edge_grad).
  * tab: ht(r) = h3(r) f_cut(r) per knot interval, float4 (a0..a3) [M - 1][64], built by mm_spline_coeffs_flat from
- * mm_radial_mlp_f64 samples (D = 64 features, last layer = identity). */
-int mm_ace1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S, int S_pad,
+ * mm_radial_mlp_f64 samples (D = 64 features, last layer = identity).  e_u: float4 (unit vector, r) per edge (as
+ * written by mm_edge_geom_*); the harmonics Y(u) are evaluated in the kernels. */
+int mm_ace1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* tab, int S, int S_pad,
                 float* B, float* rho, mm_stream_t stream);
-int mm_ace1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S, int S_pad,
+int mm_ace1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* tab, int S, int S_pad,
                 const float* gB, float inv_h, float* part, mm_stream_t stream);
 int mm_spline_coeffs_flat(const double* samples, int M, int D, double eps, double h, int tab, float* coef,
                           mm_stream_t stream);

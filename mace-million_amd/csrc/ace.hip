@@ -8,6 +8,10 @@
 // (the reference's ace_layer1.py:1-104 states the identity).  The per-edge work is the outer product ht x Y;
 // the 64 -> 128-channel maps (and the following linear / skip_tp) become one GEMM per atom (mm_linear).
 //
+// Harmonics: both kernels read the 16-byte edge vector (unit vector, r) and evaluate Y(u) once per edge: lane j of
+// a wave evaluates edge eb + j of a 64-edge batch into the wave's LDS rows (16 floats per edge), from which the
+// MFMA operands are read (instead of storing and re-reading 64 B of harmonics per edge in global memory).
+//
 // mm_ace1_fwd: one wave per receiver; B_i accumulated with v_mfma_f32_16x16x4f32 taking 4 edges per step:
 //   A operand (16 q x 4 edges) = ht, lane (i, g) -> q = 16 mt + i of edge g; B operand (4 edges x 16 m) = Y.
 //   Output layout B[i][m][s * 64 + q] (S_pad species blocks, pad species written as 0), rho[i] = sum of the edge
@@ -17,16 +21,40 @@
 //   B operand = gB), then a 16-lane sum over m.  Writes part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m.
 // ht is a cubic spline per knot interval: float4 (a0..a3) coef[row][64], row = table * (M - 1) + interval.
 #include "common.h"
+#include "gen/sh.h"
 
 #define MM_ACE_H 64
 #define MM_ACE_MAX_S 4
+#define MM_ACE_YB 64   // edges per harmonic batch (one per lane)
+
+// lane j: harmonics of edge eb + j (if it exists) into yrow[j * 16 .. + 15]; the edge vector of the next batch is
+// loaded one batch ahead (u_next)
+__device__ __forceinline__ void mm_ace_y_batch(int eb, int e1, int lane, const floatx4* __restrict__ e_u,
+                                               floatx4& u_next, float* __restrict__ yrow) {
+  mm_wave_lds_sync();   // the previous batch has been read
+  const int ej = eb + lane;
+  if (ej < e1) {
+    const floatx4 u = u_next;
+    if (ej + MM_ACE_YB < e1) u_next = e_u[ej + MM_ACE_YB];
+    float Y[16];
+    mm_sh16(u.x, u.y, u.z, Y);
+    floatx4* __restrict__ d = (floatx4*)(yrow + lane * 16);
+    d[0] = floatx4{Y[0], Y[1], Y[2], Y[3]};
+    d[1] = floatx4{Y[4], Y[5], Y[6], Y[7]};
+    d[2] = floatx4{Y[8], Y[9], Y[10], Y[11]};
+    d[3] = floatx4{Y[12], Y[13], Y[14], Y[15]};
+  }
+  mm_wave_lds_sync();
+}
 
 template <int S>
 __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict__ rowptr, int nC,
                                                           const floatx4* __restrict__ e_pk,
-                                                          const float* __restrict__ e_Y,
+                                                          const floatx4* __restrict__ e_u,
                                                           const floatx4* __restrict__ tab, int S_pad,
                                                           float* __restrict__ Bout, float* __restrict__ rho) {
+  __shared__ float yrows[4 * MM_ACE_YB * 16];
+  float* __restrict__ yrow = yrows + (threadIdx.x >> 6) * (MM_ACE_YB * 16);
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= nC) return;
   const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
@@ -37,18 +65,16 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[s][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float dsum = 0.f;
-  // the packed record and harmonic of the next step are loaded one step ahead
+  // the packed record of the next step is loaded one step ahead
   floatx4 pk_n = e0 + g < e1 ? e_pk[e0 + g] : floatx4{0.f, 0.f, 0.f, 0.f};
-  float y_n = e0 + g < e1 ? e_Y[(size_t)(e0 + g) * 16 + i16] : 0.f;
+  floatx4 u_next = e0 + lane < e1 ? e_u[e0 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
   for (int kb = e0; kb < e1; kb += 4) {
+    if (((kb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch(kb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
     const int e = kb + g;
     const bool valid = e < e1;
     const floatx4 pk = pk_n;
-    const float y = valid ? y_n : 0.f;
-    if (e + 4 < e1) {
-      pk_n = e_pk[e + 4];
-      y_n = e_Y[(size_t)(e + 4) * 16 + i16];
-    }
+    const float y = valid ? yrow[((e - e0) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
+    if (e + 4 < e1) pk_n = e_pk[e + 4];
     const int se = valid ? __float_as_int(pk.z) : -1;
     const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
     const float t = pk.x;
@@ -79,10 +105,12 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
 template <int S>
 __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict__ rowptr, int nC,
                                                           const floatx4* __restrict__ e_pk,
-                                                          const float* __restrict__ e_Y,
+                                                          const floatx4* __restrict__ e_u,
                                                           const floatx4* __restrict__ tab, int S_pad,
                                                           const float* __restrict__ gB, float inv_h,
                                                           float* __restrict__ part) {
+  __shared__ float yrows[4 * MM_ACE_YB * 16];
+  float* __restrict__ yrow = yrows + (threadIdx.x >> 6) * (MM_ACE_YB * 16);
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= nC) return;
   const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
@@ -96,7 +124,9 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
     for (int k = 0; k < 16; ++k) gb[s][k] = gp[s * MM_ACE_H + 4 * k];
   // the packed record of the next tile is loaded one tile ahead; the tile's harmonics before its MFMAs
   floatx4 pk_n = e0 + i16 < e1 ? e_pk[e0 + i16] : floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 u_next = e0 + lane < e1 ? e_u[e0 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
   for (int tb = e0; tb < e1; tb += 16) {
+    if (((tb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch(tb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
     const int e = tb + i16;          // A-operand row: edge i16 of the tile
     const bool valid = e < e1;
     const floatx4 pk = pk_n;
@@ -105,7 +135,7 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int ev = tb + 4 * g + v;
-      yv[v] = ev < e1 ? e_Y[(size_t)ev * 16 + i16] : 0.f;
+      yv[v] = ev < e1 ? yrow[((ev - e0) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
     }
     const int se = valid ? __float_as_int(pk.z) : -1;
     const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + g;
@@ -138,43 +168,45 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
 }
 
 template <int S>
-static void launch_fwd(dim3 grid, hipStream_t stream, const int* rowptr, int nC, const float* e_pk, const float* e_Y,
+static void launch_fwd(dim3 grid, hipStream_t stream, const int* rowptr, int nC, const float* e_pk, const float* e_u,
                        const float* tab, int S_pad, float* Bout, float* rho) {
-  hipLaunchKernelGGL(mm_ace1_fwd_kernel<S>, grid, dim3(256), 0, stream, rowptr, nC, (const floatx4*)e_pk, e_Y,
+  hipLaunchKernelGGL(mm_ace1_fwd_kernel<S>, grid, dim3(256), 0, stream, rowptr, nC, (const floatx4*)e_pk,
+                     (const floatx4*)e_u,
                      (const floatx4*)tab, S_pad, Bout, rho);
 }
 
 template <int S>
-static void launch_bwd(dim3 grid, hipStream_t stream, const int* rowptr, int nC, const float* e_pk, const float* e_Y,
+static void launch_bwd(dim3 grid, hipStream_t stream, const int* rowptr, int nC, const float* e_pk, const float* e_u,
                        const float* tab, int S_pad, const float* gB, float inv_h, float* part) {
-  hipLaunchKernelGGL(mm_ace1_bwd_kernel<S>, grid, dim3(256), 0, stream, rowptr, nC, (const floatx4*)e_pk, e_Y,
+  hipLaunchKernelGGL(mm_ace1_bwd_kernel<S>, grid, dim3(256), 0, stream, rowptr, nC, (const floatx4*)e_pk,
+                     (const floatx4*)e_u,
                      (const floatx4*)tab, S_pad, gB, inv_h, part);
 }
 
-extern "C" int mm_ace1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S,
+extern "C" int mm_ace1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* tab, int S,
                            int S_pad, float* B, float* rho, hipStream_t stream) {
   MM_CHECK_ARG(nC >= 0 && S >= 1 && S <= MM_ACE_MAX_S && S_pad >= S, "bad sizes (1 <= S <= 4, S_pad >= S)");
   if (nC == 0) return MM_OK;
   const dim3 grid((nC + 3) / 4);
   switch (S) {
-    case 1: launch_fwd<1>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
-    case 2: launch_fwd<2>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
-    case 3: launch_fwd<3>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
-    default: launch_fwd<4>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, B, rho); break;
+    case 1: launch_fwd<1>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, B, rho); break;
+    case 2: launch_fwd<2>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, B, rho); break;
+    case 3: launch_fwd<3>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, B, rho); break;
+    default: launch_fwd<4>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, B, rho); break;
   }
   return mm::launch_status("mm_ace1_fwd");
 }
 
-extern "C" int mm_ace1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_Y, const float* tab, int S,
+extern "C" int mm_ace1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* tab, int S,
                            int S_pad, const float* gB, float inv_h, float* part, hipStream_t stream) {
   MM_CHECK_ARG(nC >= 0 && S >= 1 && S <= MM_ACE_MAX_S && S_pad >= S, "bad sizes (1 <= S <= 4, S_pad >= S)");
   if (nC == 0) return MM_OK;
   const dim3 grid((nC + 3) / 4);
   switch (S) {
-    case 1: launch_bwd<1>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
-    case 2: launch_bwd<2>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
-    case 3: launch_bwd<3>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
-    default: launch_bwd<4>(grid, stream, rowptr, nC, e_pk, e_Y, tab, S_pad, gB, inv_h, part); break;
+    case 1: launch_bwd<1>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, gB, inv_h, part); break;
+    case 2: launch_bwd<2>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, gB, inv_h, part); break;
+    case 3: launch_bwd<3>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, gB, inv_h, part); break;
+    default: launch_bwd<4>(grid, stream, rowptr, nC, e_pk, e_u, tab, S_pad, gB, inv_h, part); break;
   }
   return mm::launch_status("mm_ace1_bwd");
 }

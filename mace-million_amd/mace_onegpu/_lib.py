@@ -11,6 +11,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libmace_million_amd.so")
+ABI_VERSION = 3     # mm_version() of the library this binding's buffer layouts are written for
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -101,11 +102,15 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"MI355X kernel library not built: {LIB_PATH} is missing "
                                "(run python mace-million_amd/build.py)")
-        _lib = ctypes.CDLL(LIB_PATH)
+        so = ctypes.CDLL(LIB_PATH)
         for name, argt in SIGNATURES.items():
-            f = getattr(_lib, name)
+            f = getattr(so, name)
             f.argtypes = argt
             f.restype = ctypes.c_char_p if name == "mm_last_error" else ctypes.c_int
+        if so.mm_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has argument conventions version {so.mm_version()}, this binding needs "
+                               f"{ABI_VERSION}: rebuild it (python mace-million_amd/build.py)")
+        _lib = so
     return _lib
 
 

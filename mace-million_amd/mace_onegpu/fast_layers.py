@@ -298,7 +298,6 @@ class FastLayers:
         i = dict(dtype=torch.int32, device=dev)
         ws = dict(nC=nC, nN=n_nodes, E=E)
         ws.update(e_u=torch.empty(E, 4, **f), e_pk=torch.empty(E, 4, **f),
-                  e_Y=torch.empty(E, 16, **f) if self.ace else None,
                   e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
         ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
                   rho=torch.empty(nC, **f), g_rho=torch.empty(nC, **f),
@@ -328,15 +327,14 @@ class FastLayers:
         ws = self.ws
         sp = self.spec
         x_from_spec = 1 if k == 0 else 0          # layer-1 sender features depend on the species only
-        e_Y = ws["e_Y"] if (k == 0 and self.ace) else None
         if g.rij is not None:
             K.mm_edge_geom_rij(g.nE, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
                                sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo, self.inv_h, x_from_spec,
-                               ws["e_u"], e_Y, ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
+                               ws["e_u"], None, ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
         else:
             K.mm_edge_geom_pos(g.nE, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
                                self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo,
-                               self.inv_h, x_from_spec, ws["e_u"], e_Y, ws["e_pk"], ws["e_recv"],
+                               self.inv_h, x_from_spec, ws["e_u"], None, ws["e_pk"], ws["e_recv"],
                                ws["e_dd"], stream())
 
     def prepare(self, g):
@@ -362,7 +360,7 @@ class FastLayers:
         self._geometry(0, g)
         if self.ace:
             Kp = self.ace_Kp
-            self._timed("ace1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_ace1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+            self._timed("ace1_fwd", (g.nE, g.nC, g.n_nodes), K.mm_ace1_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                         self.tab_h, self.S, self.S_pad, ws["A"], rho_out, stream())
             self._lin(self.plan_ace, ws["A"], 16 * Kp, M_out, 16 * C, self.W_ace, g.nC, scale=rho_out, scale_mode=1,
                       species=True, w_group_stride=4 * self.ace_nJ)
@@ -405,7 +403,7 @@ class FastLayers:
             Kp = self.ace_Kp
             self._lin(self.plan_aceT, ws["gM"], 16 * C, ws["gA"], 16 * Kp, self.W_aceT, g.nC, scale=rho,
                       scale_mode=1, species=True, w_group_stride=4 * self.ace_nJ)
-            self._timed("ace1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_ace1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_Y"],
+            self._timed("ace1_bwd", (g.nE, g.nC, g.n_nodes), K.mm_ace1_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                         self.tab_h, self.S, self.S_pad, ws["gA"], self.inv_h, ws["part"], stream())
             n_part = 1
         else:

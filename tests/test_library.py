@@ -27,7 +27,21 @@ def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(LIB)
     missing = [s for s in declared() if not hasattr(lib, s)]
     assert not missing, missing
-    assert lib.mm_version() >= 1
+    from mace_onegpu import _lib
+    assert lib.mm_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (python mace-million_amd/build.py)")
+def test_binding_refuses_a_library_of_other_conventions(monkeypatch):
+    """A library whose argument conventions differ from the binding's (an older build given newer buffer layouts)
+    is refused when it is loaded, before any kernel can read a buffer with the wrong layout."""
+    from mace_onegpu import _lib
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "ABI_VERSION", _lib.ABI_VERSION + 1)
+    with pytest.raises(RuntimeError, match="argument conventions version"):
+        _lib.lib()
+    monkeypatch.undo()
+    assert _lib.lib().mm_version() == _lib.ABI_VERSION
 
 
 def test_generated_sources_are_current(tmp_path):
