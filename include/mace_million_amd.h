@@ -61,8 +61,8 @@ int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] *
 /* ---------------------------------------------------------------------------------------------- edge geometry
  * Replace receiver_chunk_mace.edge_embed (:230-234), the table coordinates of spline_w._coords (spline_w.py:18-27)
  * and the density part of FastLayers.layer1/layer2_energy (fast_layers.py:179-183, 190-192, 209-213): per edge
- * e_u float4 (unit vector, length; the convolutions evaluate Y_lm l<=3 from it), optionally the 16 harmonics e_Y
- * (for the layer-1 ACE kernels), the local receiver, and a packed
+ * e_u float4 (unit vector, length; the convolutions and the ACE kernels evaluate Y_lm l<=3 from it), optionally
+ * the 16 harmonics e_Y (nullable; the production path passes null), the local receiver, and a packed
  * float4 (t, spline interval row of the ordered species pair's table, sender feature row (its species when
  * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).  dens_w is HOST [nb]. */
 int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* local_send,

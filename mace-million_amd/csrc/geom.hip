@@ -1,9 +1,9 @@
 // Per-edge geometry of a receiver chunk and the per-edge gradient assembly.
 //
 // mm_edge_geom_rij / mm_edge_geom_pos: edge vector (fp64 in, fp32 out, as the reference's rij.to(dtype),
-// mliap_threepass.py:326) stored as (unit vector, length) -- the convolutions evaluate the spherical harmonics from
-// it; e_Y (optional, for the layer-1 ACE kernels) receives the 16 harmonics --, local receiver index, and one packed
-// record per edge
+// mliap_threepass.py:326) stored as (unit vector, length) -- the convolutions and the ACE kernels evaluate the
+// spherical harmonics from it; e_Y (optional, null on the production path) receives the 16 harmonics --, local
+// receiver index, and one packed record per edge
 // for the convolutions: (t, spline interval row = table(pair) * (M - 1) + k, feature row of the sender, edge
 // density d = tanh((B(r) . w / sqrt(nb))^2) f_cut(r)) (fast_layers.py:154-156, 179-183, 190-192); d'(r) separately.
 // mm_edge_grad: dL/dv_e = dL/dr u + (I - u u^T) grad_u(sum_m dL/dY_m Y_m) / r, with dL/dr and dL/dY summed
