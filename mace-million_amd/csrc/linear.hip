@@ -15,7 +15,9 @@
 // Six 16x16x32 bf16 products take 96 cycles against 256 for the same K = 32 in v_mfma_f32_16x16x4f32.  The
 // weights are split once on the host; the input rows are split as they are loaded.
 //
-// Launch: grid (ceil(rows / (256 n_blk)), n_comp, n_groups); 1024 threads = 16 waves, each wave 16 rows x 128
+// Launch: grid (n_comp, ceil(rows / (256 n_blk)), n_groups), components fastest: the workgroups of one row block
+// are dispatched together, so an output row is written and an input row is read by neighbouring workgroups
+// (measured: 4-15 % less linear time than row blocks fastest).  1024 threads = 16 waves, each wave 16 rows x 128
 // columns (8 MFMA tiles) of each of its n_blk row blocks; the weight block (3 bf16 planes of 128 x 128, 96 KiB)
 // is staged in LDS in the lane order of the B operand.  16 waves of one workgroup per CU = 4 waves per SIMD.
 // Weight blocks: plane p of block b at bf16 offset (3 b + p) 16384; element W[k][n], k = 32 t + 8 g + u,
@@ -100,10 +102,10 @@ __device__ __forceinline__ void mm_split3_bf16(const floatx8& x, bf16x8& x0, bf1
 // is staged in LDS once for all of them.
 __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs args, int n_blk) {
   __shared__ uint4 Wl[3 * 2048];
-  const MMLinComp& cp = args.comp[blockIdx.y];   // kernel-argument memory, read with uniform indices
+  const MMLinComp& cp = args.comp[blockIdx.x];   // kernel-argument memory, read with uniform indices
   const int grp = blockIdx.z;
   const int nrows = args.list ? args.list_count[grp] : args.n_rows;
-  const int blk0 = blockIdx.x * n_blk;
+  const int blk0 = blockIdx.y * n_blk;
   if (blk0 * MM_LIN_BLOCK_ROWS >= nrows) return;
   const int blk1 = min(blk0 + n_blk, (nrows + MM_LIN_BLOCK_ROWS - 1) / MM_LIN_BLOCK_ROWS);
   const int* __restrict__ list = args.list ? args.list + (size_t)grp * args.list_stride : nullptr;
@@ -214,7 +216,7 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
   const long n_blocks = (n_rows_max + MM_LIN_BLOCK_ROWS - 1) / MM_LIN_BLOCK_ROWS;
   const long per_blk = (long)n_comp * n_groups;
   const int n_blk = (int)std::max(1L, std::min(8L, n_blocks * per_blk / MM_LIN_MIN_WG));
-  dim3 grid((unsigned)((n_blocks + n_blk - 1) / n_blk), n_comp, n_groups);
+  dim3 grid(n_comp, (unsigned)((n_blocks + n_blk - 1) / n_blk), n_groups);
   hipLaunchKernelGGL(mm_linear_kernel, grid, dim3(64 * MM_LIN_NW), 0, stream, a, n_blk);
   return mm::launch_status("mm_linear");
 }
