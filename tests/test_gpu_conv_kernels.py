@@ -29,9 +29,9 @@ def _terms():
     return mm.Tables(mm.MaceSpec()).tp2
 
 
-def _case(seed, nC, n_nodes, deg_max, local, NR=9):
+def _case(seed, nC, n_nodes, deg_max, local, NR=9, degrees=None):
     rng = np.random.default_rng(seed)
-    deg = rng.integers(0, deg_max + 1, nC)
+    deg = rng.integers(0, deg_max + 1, nC) if degrees is None else rng.choice(degrees, nC)
     deg[::7] = 0
     send = []
     for i in range(nC):
@@ -88,16 +88,18 @@ def _reference(cs, tp):
     return out.detach(), rho, X.grad.reshape(-1, 4 * C), Y.grad, t.grad
 
 
-@pytest.mark.parametrize("name,nC,n_nodes,deg_max,local", [
-    ("local", 203, 1500, 120, True),        # 203 = 50 groups of 4 + a group of 3
-    ("scattered", 97, 4000, 240, False),    # distinct senders per group > slots; edges per group > cap
-    ("sparse", 61, 300, 6, False),          # few edges, many empty receivers
+@pytest.mark.parametrize("name,nC,n_nodes,deg_max,local,degrees", [
+    ("local", 203, 1500, 120, True, None),        # 203 = 50 groups of 4 + a group of 3
+    ("scattered", 97, 4000, 240, False, None),    # distinct senders per group > slots; edges per group > cap
+    ("sparse", 61, 300, 6, False, None),          # few edges, many empty receivers
+    # receivers at and around the forward's 64-edge batches of harmonic factors
+    ("batch_edges", 67, 1200, 0, False, [1, 3, 4, 5, 63, 64, 65, 127, 128, 129, 192]),
 ])
-def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local):
+def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local, degrees):
     from mace_onegpu._lib import K, stream
     assert torch.cuda.is_available(), "GPU test without a GPU"
     tp = _terms()
-    cs = _case(7, nC, n_nodes, deg_max, local)
+    cs = _case(7, nC, n_nodes, deg_max, local, degrees=degrees)
     E = len(cs["send"])
     print(f"case {name}: nC {nC} nodes {n_nodes} edges {E}", flush=True)
     dev = "cuda"
