@@ -83,8 +83,12 @@ class _Fn:
 
     def __call__(self, *args):
         conv = []
-        for a in args:
+        for k, a in enumerate(args):
             if isinstance(a, torch.Tensor):
+                # tensors are device buffers; the HOST arrays of the ABI are passed as ctypes objects
+                if a.device.type != "cuda":
+                    raise TypeError(f"{self.name}: argument {k} is a {a.device.type} tensor; the kernels take "
+                                    "device memory")
                 conv.append(ctypes.c_void_p(a.data_ptr()))
             elif a is None:
                 conv.append(ctypes.c_void_p(0))

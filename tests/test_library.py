@@ -44,6 +44,19 @@ def test_binding_refuses_a_library_of_other_conventions(monkeypatch):
     assert _lib.lib().mm_version() == _lib.ABI_VERSION
 
 
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (python mace-million_amd/build.py)")
+def test_binding_refuses_host_tensors():
+    """A CPU tensor handed to a kernel entry point is refused before the call (its address is not device memory;
+    the ABI's HOST arrays are ctypes objects, not tensors)."""
+    import torch
+
+    from mace_onegpu._lib import K
+    x = torch.zeros(16)
+    with pytest.raises(TypeError, match="argument 0 is a cpu tensor"):
+        K.mm_fill_f32(x, 16, 1.0, None)
+    assert not x.any()
+
+
 def test_generated_sources_are_current(tmp_path):
     from mace_onegpu import codegen, model
     codegen.generate(str(tmp_path), model.Tables(model.MaceSpec()))
