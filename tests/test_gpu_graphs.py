@@ -62,6 +62,36 @@ def test_mliap_graphs_match_eager(model, water_sys, cache_l1, monkeypatch):
     assert graphed.n_captures == 1
 
 
+def test_mliap_graphs_recapture_when_a_call_outgrows_them(model, water_sys, monkeypatch):
+    """A call whose chunks and ghost count exceed the captured capacities (no headroom: margin 1.0, edge capacity
+    aligned to 256) recaptures once; a smaller call after it replays the larger graphs.  Every call equals the eager
+    evaluation of the same input."""
+    from mace_onegpu import systems
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    from mace_onegpu.receiver_chunk_mace import System
+    pos, box, Z = systems.water_box(512, seed=2)
+    big = System(pos, box, Z - 1, 6.0, "cuda")
+    big.build_neighbors()
+    monkeypatch.setenv("MACE3P_CAP_MARGIN", "1.0")
+    monkeypatch.setenv("MACE3P_GRAPHS", "0")
+    eager = ThreePassMLIAP(model, chunk=48, e_align=256)
+    monkeypatch.setenv("MACE3P_GRAPHS", "1")
+    graphed = ThreePassMLIAP(model, chunk=48, e_align=256)
+    captures = []
+    for call, s in enumerate((water_sys, big, water_sys)):
+        _say(f"case mliap graphs recapture call {call}: {s.N} atoms")
+        d0 = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True)
+        eager.compute_forces(d0)
+        torch.cuda.synchronize()
+        d1 = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True)
+        graphed.compute_forces(d1)
+        torch.cuda.synchronize()
+        captures.append(graphed.n_captures)
+        _close(d1.energy, d1.pair_forces, d1.eatoms, d0.energy, d0.pair_forces, d0.eatoms, s.N, f"call {call}")
+    assert captures == [1, 2, 2]
+
+
 def test_standalone_graphs_match_eager(model, water_sys):
     """ReceiverChunkMACE(use_graphs=True): 3 full chunks of 64 receivers, two calls, and a translated copy of the
     box (same capacities, new positions) -- every call equal to the eager evaluation of the same input."""
