@@ -79,10 +79,16 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
     const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
     const float t = pk.x;
     if (i16 == 0 && valid) dsum += pk.w;
+    // the step's four table rows are loaded together, before any use: an invalid lane reads row 0 (finite) and
+    // its h is zeroed by a factor, so no load sits behind a branch on the edge's validity
+    const float vf = valid ? 1.f : 0.f;
+    floatx4 c[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) c[mt] = tp[16 * mt];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const floatx4 c = tp[16 * mt];
-      const float h = valid ? fmaf(fmaf(fmaf(c.w, t, c.z), t, c.y), t, c.x) : 0.f;
+      const float h = vf * fmaf(fmaf(fmaf(c[mt].w, t, c[mt].z), t, c[mt].y), t, c[mt].x);
 #pragma unroll
       for (int s = 0; s < S; ++s)
         acc[s][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? h : 0.f, y, acc[s][mt], 0, 0, 0);
