@@ -150,23 +150,44 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
         }
       }
     }
-    // D layout of the 16x16 tile: lane (i, g) holds rows 4 g + v (v = 0..3) of column i
+    // D layout of the 16x16 tile: lane (i, g) holds rows 4 g + v (v = 0..3) of column i.  The row indices and
+    // scales of the four rows are loaded before any store, and an accumulating launch reads the eight old values
+    // of a row together (one memory round trip per row, not one per value).  A lane past the last row uses
+    // logical row 0 (there is one) for its loads and stores nothing.
+    bool ok[4];
+    int id[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int rr = row0 + wave * 16 + 4 * g + v;
-      if (rr >= nrows) continue;
-      const int id = list ? list[rr] : rr;
-      const long orow = args.out_rows ? (long)args.out_rows[id] : (long)id;
-      float s = 1.f;
-      if (args.row_scale) s = args.scale_mode == 1 ? 1.f / (args.row_scale[id] + 1.f) : args.row_scale[id];
-      float* __restrict__ op = args.out + orow * args.out_stride + cp.out_off + i;
+      ok[v] = rr < nrows;
+      id[v] = ok[v] ? (list ? list[rr] : rr) : 0;
+    }
+    float* op[4];
+    float sc[4];
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        const float val = s * acc[nt][v];
-        if (args.accumulate)
-          op[16 * nt] += val;
-        else
-          op[16 * nt] = val;
+    for (int v = 0; v < 4; ++v) {
+      const long orow = args.out_rows ? (long)args.out_rows[id[v]] : (long)id[v];
+      op[v] = args.out + orow * args.out_stride + cp.out_off + i;
+      sc[v] = 1.f;
+      if (args.row_scale)
+        sc[v] = args.scale_mode == 1 ? 1.f / (args.row_scale[id[v]] + 1.f) : args.row_scale[id[v]];
+    }
+    if (args.accumulate) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (!ok[v]) continue;
+        float old[8];
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) old[nt] = op[v][16 * nt];
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) op[v][16 * nt] = old[nt] + sc[v] * acc[nt][v];
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (!ok[v]) continue;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) op[v][16 * nt] = sc[v] * acc[nt][v];
       }
     }
     if (blk + 1 < blk1) mm_lin_rows(args, list, nrows, row0 + MM_LIN_BLOCK_ROWS, wave, i, rw);
