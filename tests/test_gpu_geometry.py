@@ -1,0 +1,79 @@
+"""mm_edge_geom_rij called through the C ABI on random pair vectors, against the fp64 oracle (marked gpu).
+
+Semantics checked (fast_layers.py:154-156, 179-183, 190-192; spline_w._coords, spline_w.py:18-27):
+    e_u[e]  = (v / |v|, |v|),  v = rij[e] rounded to fp32 (rij.to(dtype), mliap_threepass.py:326)
+    e_pk[e] = (t, table(pair) * (M - 1) + k, sender feature row, d(|v|)),  x = clamp((r - r_lo) / h, 0, M - 1 - 1e-4),
+              k = floor(x), t = x - k, pair = (species(send), species(recv)), d(r) = tanh((B(r) . w)^2) f_cut(r)
+    e_dd[e] = d'(r),  e_recv[e] = pair_i[e] - a
+Lengths are drawn away from the knots (t in [0.05, 0.95]) so that the interval is the same in fp32 and fp64.
+"""
+import ctypes
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("x_from_spec", [0, 1])
+def test_edge_geometry_against_fp64(x_from_spec):
+    from mace_onegpu._lib import K, stream
+    from oracle import mace_ref
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    g = torch.Generator().manual_seed(7 + x_from_spec)
+    E, n_nodes, S, nb, p, M, r_lo, r_max = 3000, 200, 2, 8, 5, 512, 0.5, 6.0
+    h = (r_max - r_lo) / (M - 1)
+    print(f"case x_from_spec={x_from_spec}: {E} edges", flush=True)
+    k = torch.randint(0, M - 1, (E,), generator=g)
+    t = 0.05 + 0.9 * torch.rand(E, generator=g, dtype=torch.float64)
+    r = r_lo + (k + t) * h
+    r = r.clamp(max=r_max - 0.05 * h)
+    u = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    u /= u.norm(dim=1, keepdim=True)
+    rij = u * r[:, None]
+    a = 17
+    recv = torch.randint(0, n_nodes, (E,), generator=g)
+    send = torch.randint(0, n_nodes, (E,), generator=g)
+    spec = torch.randint(0, S, (n_nodes,), generator=g)
+    pair_map = torch.tensor([2, 0, 3, 1])                            # distinct table per ordered pair
+    w = torch.randn(nb, generator=g, dtype=torch.float64) * 0.3
+
+    # fp64 reference on the fp32 values the kernel reads
+    v = rij.float().double()
+    rr = v.norm(dim=1).requires_grad_()
+    wf = w.float().double()
+    d = torch.tanh((mace_ref.bessel(rr, r_max, nb) @ wf) ** 2) * mace_ref.poly_cutoff(rr, r_max, p)
+    (dd,) = torch.autograd.grad(d.sum(), rr)
+    d, rr = d.detach(), rr.detach()
+    x = ((rr - r_lo) / h).clamp(0.0, M - 1 - 1e-4)
+    kk = torch.floor(x)
+    row = pair_map[spec[send] * S + spec[recv]] * (M - 1) + kk.long()
+    xsrc = spec[send] if x_from_spec else send
+
+    dev = "cuda"
+    i32 = dict(dtype=torch.int32, device=dev)
+    e_u = torch.full((E, 4), float("nan"), device=dev)
+    e_pk = torch.full((E, 4), float("nan"), device=dev)
+    e_recv = torch.full((E,), -7, **i32)
+    e_dd = torch.full((E,), float("nan"), device=dev)
+    dens_w = (ctypes.c_float * nb)(*w.tolist())
+    K.mm_edge_geom_rij(E, rij.to(dev), (recv + a).to(**i32), a, send.to(**i32), spec.to(**i32), S,
+                       pair_map.to(**i32), dens_w, nb, r_max, p, M, r_lo, 1.0 / h, x_from_spec, e_u, None, e_pk,
+                       e_recv, e_dd, stream())
+    torch.cuda.synchronize()
+    e_u, e_pk, e_recv, e_dd = e_u.cpu().double(), e_pk.cpu(), e_recv.cpu(), e_dd.cpu().double()
+    pki = e_pk.view(torch.int32)
+
+    def close(name, got, ref, tol):
+        err = float((got - ref).abs().max())
+        print(f"  {name}: max|err| {err:.3e} (max|ref| {float(ref.abs().max()):.3e})", flush=True)
+        assert torch.isfinite(got).all() and err <= tol
+
+    close("unit vector", e_u[:, :3], v / rr[:, None], 3e-7)
+    close("r", e_u[:, 3], rr, 2e-7 * r_max)
+    close("t", e_pk[:, 0].double(), x - kk, 1e-4)
+    close("density", e_pk[:, 3].double(), d, 3e-6 * float(d.abs().max()) + 1e-7)
+    close("d density / dr", e_dd, dd, 1e-5 * float(dd.abs().max()) + 1e-7)
+    assert torch.equal(pki[:, 1].long(), row)
+    assert torch.equal(pki[:, 2].long(), xsrc)
+    assert torch.equal(e_recv.long(), recv)
