@@ -51,7 +51,9 @@ __device__ __forceinline__ void mm_density(float r, const MMDensity& dp, float& 
 }
 
 // Spline coordinate of a length r: x = clamp((r - r_lo) / h, 0, M - 1 - 1e-4), interval k = floor(x), t = x - k
-// (the clamp of spline_w._coords, spline_w.py:18-27).
+// (the clamp of spline_w._coords, spline_w.py:18-27).  The tables hold M - 1 intervals, so k is also clamped to
+// M - 2: for M >= 4096 the fp32 value M - 1 - 1e-4 rounds to M - 1, and floor(x) alone would index one interval
+// past the table (then t = x - k = 1, the right end of the last interval).
 struct MMSpline {
   int M;
   float r_lo, inv_h;
@@ -77,7 +79,7 @@ __device__ __forceinline__ void mm_geom_common(int e, float vx, float vy, float 
   }
   const int tab = pair_map[node_spec[send] * S + node_spec[recv]];
   const float x = fminf(fmaxf((r - sp.r_lo) * sp.inv_h, 0.f), (float)(sp.M - 1) - 1e-4f);
-  const float kf = floorf(x);
+  const float kf = fminf(floorf(x), (float)(sp.M - 2));
   const int row = tab * (sp.M - 1) + (int)kf;
   const int xsrc = x_from_spec ? node_spec[send] : send;
   e_recv[e] = recv;

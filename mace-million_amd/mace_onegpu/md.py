@@ -143,6 +143,7 @@ class MDRunner:
         self._build(torch.as_tensor(pos, dtype=torch.float64, device=self.dev))
         self.F = None
         self.E = None
+        self.eat = None
 
     def _build(self, pos):
         spidx = (self.Z - 1).to(torch.int32)
@@ -161,7 +162,7 @@ class MDRunner:
         pl.refresh()
         view = _PairView(pl)
         E, eat, F, PF = self.ev.compute(view)
-        self.E, self.F = E, F
+        self.E, self.eat, self.F = E, eat, F
         return E, F
 
     def _maybe_rebuild(self):

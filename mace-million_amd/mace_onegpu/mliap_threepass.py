@@ -1,17 +1,25 @@
-"""LAMMPS ML-IAP ("pair_style mliap unified <file.pt> 0") wrapper of the three-pass MACE evaluation on MI355X.
+"""LAMMPS ML-IAP ("pair_style mliap unified <file.pt> 0") plugin of the three-pass MACE evaluation on MI355X.
 
-Same class, module path, constructor, attributes and compute_forces(data) contract as the reference's
-mace_onegpu/mliap_threepass.py (ThreePassMLIAP, :155-622):
-    pass A  receiver chunks of local atoms:  h1 = layer1 (no grad)                       -> H1[local]
-            forward_exchange(H1)                                                        -> H1 on ghosts
-    pass B  chunks: E2 = layer-2 energy;  dE2/drij -> pair forces,  dE2/dh1 -> G1[local + ghost]
-            reverse_exchange(G1)                                                        -> ghost terms on owners
-    pass C  chunks: layer 1 again with gradient; loss = scale R1 + G1 . h1; d/drij -> pair forces
-H1, G1, the per-pair arrays and (MACE3P_CACHE_L1=1, the default) pass A's layer-1 message and density of every
-local atom (8 KiB per atom, so that pass C does not recompute layer 1) persist; every other wide intermediate lives
-in one chunk's workspace.  The arithmetic runs in the HIP kernels of libmace_million_amd.so
-(fast_layers.FastLayers); with MACE3P_GRAPHS=1 the passes of full chunks are captured once as HIP graphs and
-replayed per chunk (chunk_graphs.ChunkGraphExec).
+The contract is the reference's ThreePassMLIAP (mace_onegpu/mliap_threepass.py:155-622): class name, module path,
+constructor, the attributes LAMMPS reads, the fields of ``data`` read and written, the MACE3P_* knobs, and the
+guard messages with their limits.  The code behind it is organised differently:
+
+* ``_PairBatch``: the call's pairs on the device, grouped by receiver (a stable sort only when LAMMPS hands them
+  over unsorted), the receiver CSR and the inverse permutation that puts the pair forces back in LAMMPS' order;
+* ``_Runtime``: everything a force call needs that is not pickled (the kernel-side model constants of
+  fast_layers.FastLayers, the knobs read once from the environment, per-atom scratch, the pass-A layer-1 cache,
+  the HIP-graph executor of full chunks, the log); rebuilt on the first call after unpickling or when a species
+  appears that the constants were not built for;
+* ``_EagerPasses``: the eager per-chunk pipeline behind the same pass_a / pass_b / pass_c interface as the graph
+  executor (chunk_graphs.ChunkGraphExec), so the pass loop picks an executor per chunk and nothing else.
+
+The three passes (the exact algorithm of mliap_threepass.py:444-616):
+    A  every receiver chunk: h1 = layer 1 (no gradient)                 -> H1[local];  forward_exchange -> H1x
+    B  every chunk: E2 = layer-2 energy; dE2/drij -> pair forces; dE2/dh1 -> G1[local + ghost];
+       reverse_exchange -> G1r (ghost rows summed onto their owners)
+    C  every chunk: layer 1 with gradient; loss = scale R1 + G1r . h1; d/drij -> pair forces
+Persistent per call: H1, G1, the per-pair arrays and (MACE3P_CACHE_L1=1, the default) pass A's layer-1 message
+and density of every local atom (8 KiB per atom), so that pass C does not recompute layer 1.
 """
 import json
 import os
@@ -20,7 +28,7 @@ import time
 import torch
 
 from . import chunk_graphs, fast_layers
-from .receiver_chunk_mace import chunk_topology, make_chunk
+from .receiver_chunk_mace import check_chunk, chunk_topology, make_chunk
 
 try:
     from lammps.mliap.mliap_unified_abc import MLIAPUnified
@@ -36,31 +44,307 @@ CHEMICAL_SYMBOLS = [
     "Ce", "Pr", "Nd", "Pm", "Sm", "Eu", "Gd", "Tb", "Dy", "Ho", "Er", "Tm", "Yb", "Lu", "Hf", "Ta", "W", "Re", "Os",
     "Ir", "Pt", "Au", "Hg", "Tl", "Pb", "Bi", "Po", "At", "Rn", "Fr", "Ra", "Ac"]
 
-_RUNTIME = ("_fl", "_dev", "_cols", "_e0", "_loc", "_flag", "_log", "_D1", "_gx", "_use_graphs", "_fmax_abort",
-            "_t_end", "_peak", "_topo", "_cache_l1", "_l1cache")
-
-_INT_MAX = 2 ** 31 - 1
+# LAMMPS sizes its ML-IAP exchange buffers and indexes its Kokkos neighbour list with 32-bit ints
+INT32_ELEMENTS = 2 ** 31 - 1
 
 
-def _exchange(fn, src, dst, D):
-    """LAMMPS' ML-IAP comm buffers are sized with 32-bit ints (ntotal * D): split the feature columns so that every
-    call stays below 2^31 elements (mliap_threepass.py:40-55)."""
-    nt = src.shape[0]
-    if nt * D < _INT_MAX:
+def exchange_in_column_blocks(fn, src, dst, D):
+    """Calls the LAMMPS exchange fn(src, dst, D) so that no call moves INT32_ELEMENTS elements or more: the whole
+    [ntotal, D] array at once when it fits, otherwise the widest column blocks that fit (each block copied into a
+    contiguous array for the call and back into dst)."""
+    rows = int(src.shape[0])
+    if rows * D < INT32_ELEMENTS:
         fn(src, dst, D)
         return
-    w = D
-    while nt * w >= _INT_MAX and w > 1:
-        w //= 2
-    for c in range(0, D, w):
-        cw = min(w, D - c)
-        s = src[:, c:c + cw].contiguous()
-        d = torch.empty_like(s)
-        fn(s, d, cw)
-        dst[:, c:c + cw] = d
+    width = (INT32_ELEMENTS - 1) // max(rows, 1)
+    if width < 1:
+        raise RuntimeError(f"ThreePassMLIAP: {rows} rows exceed the 32-bit exchange buffers of LAMMPS even for one "
+                           f"column")
+    for c0 in range(0, D, width):
+        c1 = min(D, c0 + width)
+        block = src[:, c0:c1].contiguous()
+        out = torch.empty_like(block)
+        fn(block, out, c1 - c0)
+        dst[:, c0:c1].copy_(out)
+
+
+def neighbour_slot_guard(nlocal, npairs, rcutfac):
+    """Raises before any work when LAMMPS' int32-indexed neighbour list (pairs inside r_max grown by the skin
+    shell, on average ((r_max + skin) / r_max)^3) would come within 5 % of 2^31 slots; MACE3P_ALLOW_HUGE=1 lifts
+    it (mliap_threepass.py:450-461)."""
+    skin = float(os.environ.get("MACE3P_SKIN", "2.0"))
+    r_max = 2.0 * rcutfac
+    slots = npairs * ((r_max + skin) / r_max) ** 3
+    if slots <= 0.95 * 2 ** 31 or os.environ.get("MACE3P_ALLOW_HUGE", "0") == "1":
+        return
+    raise RuntimeError(f"ThreePassMLIAP guard: nlocal={nlocal:,}, pairs={npairs:,} -> estimated LAMMPS neighbour slots "
+                       f"{slots:.3e} is close to the 2^31 int32 limit of the Kokkos neighbour list "
+                       f"(skin {skin} A). Use fewer atoms per GPU, a smaller skin, or more GPUs.")
+
+
+def output_guard(eat, PF, limit, call):
+    """Raises instead of handing LAMMPS non-finite energies or a pair force beyond `limit` eV/A
+    (MACE3P_FMAX_ABORT, mliap_threepass.py:595-601)."""
+    fmax = float(PF.abs().max()) if PF.numel() else 0.0
+    if bool(torch.isfinite(eat).all()) and fmax == fmax and fmax < limit:
+        return
+    raise RuntimeError(f"ThreePassMLIAP guard: non-finite or absurd output at call {call} "
+                       f"(max |pair force| = {fmax:.3e} eV/A, limit {limit:g}); aborting before LAMMPS "
+                       f"integrates it. The model is probably extrapolating (check the trajectory / training data).")
+
+
+class _Knobs:
+    """The MACE3P_* environment knobs, read once when the runtime is built."""
+
+    def __init__(self):
+        env = os.environ.get
+        self.chunk = int(env("MACE3P_CHUNK")) if env("MACE3P_CHUNK") else None
+        self.fmax_abort = float(env("MACE3P_FMAX_ABORT", "100.0"))
+        self.cache_layer1 = env("MACE3P_CACHE_L1", "1") == "1"
+        self.graphs = env("MACE3P_GRAPHS", "0") == "1"
+        self.cap_margin = float(env("MACE3P_CAP_MARGIN", "1.25"))
+        self.ace_layer1 = env("MACE3P_ACE_L1", "1") == "1"
+        self.check = env("MACE3P_CHECK", "0") == "1"
+        self.log_path = env("MACE3P_LOG")
+
+
+class _PairBatch:
+    """One call's pairs on the device, grouped by receiver.
+
+    LAMMPS may hand the pairs over in any order; the kernels need them grouped by receiver (pair_i).  When they
+    are not already non-decreasing they are put in that order by a stable sort, and `restore` applies the inverse
+    permutation to the per-pair results.  rowptr [nlocal + 1] is the receiver CSR (its host copy is the call's
+    one device-to-host read)."""
+
+    def __init__(self, data, nlocal, ntotal, dev, check):
+        pi = torch.as_tensor(data.pair_i).to(dev).to(torch.int32)
+        pj = torch.as_tensor(data.pair_j).to(dev).to(torch.int32)
+        rij = torch.as_tensor(data.rij).to(dev).to(torch.float64)
+        self.perm = None
+        if pi.numel() > 1 and bool((pi[1:] < pi[:-1]).any()):
+            pi, self.perm = torch.sort(pi, stable=True)
+            pj, rij = pj[self.perm], rij[self.perm]
+        self.pair_i, self.pair_j, self.rij = pi.contiguous(), pj.contiguous(), rij.contiguous()
+        if check:
+            lo_i, hi_i = (int(pi.min()), int(pi.max())) if pi.numel() else (0, 0)
+            lo_j, hi_j = (int(pj.min()), int(pj.max())) if pj.numel() else (0, 0)
+            if lo_i < 0 or hi_i >= nlocal or lo_j < 0 or hi_j >= ntotal:
+                raise ValueError(f"ThreePassMLIAP: pair_i in [{lo_i}, {hi_i}] must lie in [0, {nlocal}) and "
+                                 f"pair_j in [{lo_j}, {hi_j}] in [0, {ntotal})")
+        counts = torch.bincount(pi.long(), minlength=nlocal)
+        if counts.numel() != nlocal:
+            raise ValueError(f"ThreePassMLIAP: a pair receiver is not a local atom (nlocal = {nlocal})")
+        self.rowptr = torch.zeros(nlocal + 1, dtype=torch.int64, device=dev)
+        self.rowptr[1:] = torch.cumsum(counts, 0)
+        self.rowptr_host = self.rowptr.cpu().numpy()
+
+    def restore(self, per_pair):
+        """Per-pair results back in the order the pairs arrived in."""
+        if self.perm is None:
+            return per_pair
+        return torch.empty_like(per_pair).index_copy_(0, self.perm, per_pair)
+
+
+class _EagerPasses:
+    """The per-chunk pipelines of fast_layers.FastLayers on freshly allocated call buffers, behind the pass
+    interface of chunk_graphs.ChunkGraphExec."""
+
+    def __init__(self, fl, call):
+        self.fl, self.call = fl, call
+
+    def pass_a(self, g):
+        self.fl.pass_a(g, self.call.H1, self.call.cache)
+
+    def pass_b(self, g):
+        c = self.call
+        self.fl.pass_b(g, c.H1x, c.G1, c.PF, c.eat)
+
+    def pass_c(self, g):
+        c = self.call
+        if c.cache is None:
+            self.fl.pass_c(g, c.G1r, c.PF, c.eat)
+        else:
+            self.fl.pass_c(g, c.G1r, c.PF, c.eat, c.H1x, c.cache)
+
+
+class _CallBuffers:
+    """Per-call arrays: views of the graph executor's static buffers when full chunks are replayed (its graphs
+    read and write them in place), otherwise fresh allocations released as soon as the passes are done with
+    them."""
+
+    def __init__(self, rt, nl, nt, P, gx):
+        dev, D1 = rt.dev, rt.D1
+        self.PF = torch.zeros(P, 3, dtype=torch.float32, device=dev)
+        self.gx = gx
+        if gx is not None:
+            self.H1, self.H1x, self.G1, self.G1r = gx.H1[:nt], gx.H1x[:nt], gx.G1[:nt], gx.G1r[:nt]
+            self.eat = gx.eat[:nl]
+            self.cache = gx.cache()
+            self.H1.zero_()
+        else:
+            self.H1 = torch.zeros(nt, D1, dtype=torch.float32, device=dev)
+            self.H1x = self.G1 = self.G1r = None
+            self.eat = torch.zeros(nl, dtype=torch.float64, device=dev)
+            self.cache = rt.layer1_cache(nl)
+
+    def after_pass_a(self):
+        if self.gx is None:
+            self.H1x = torch.empty_like(self.H1)
+
+    def before_pass_b(self):
+        if self.gx is None:
+            self.H1 = None                                  # H1x holds everything pass B and C read
+            self.G1 = torch.zeros_like(self.H1x)
+        else:
+            self.G1.zero_()
+            self.eat.zero_()                                # the captures of this call wrote into eat
+
+    def after_pass_b(self):
+        if self.gx is None:
+            self.G1r = torch.empty_like(self.G1)
+            if self.cache is None:
+                self.H1x = None                             # pass C recomputes h1: H1x is no longer read
+
+    def before_pass_c(self):
+        if self.gx is None:
+            self.G1 = None
+
+
+class _Runtime:
+    """What a force call needs that is not pickled, for one device and one set of present species."""
+
+    def __init__(self, plugin, elems, dev):
+        self.knobs = k = _Knobs()
+        self.dev = dev
+        self.cols = sorted(int(c) for c in torch.unique(elems).tolist())
+        model = plugin.model.to(dev).eval()
+        for p in model.parameters():
+            p.requires_grad_(False)
+        plugin.model = model
+        self.fl = fast_layers.FastLayers(model, self.cols, spline_grid=plugin.spline_grid, device=dev,
+                                         ace_layer1=k.ace_layer1)
+        self.scale, self.shift, self.e0 = self.fl.scale, self.fl.shift, self.fl.e0
+        self.D1 = 4 * model.spec.C
+        self.chunk = k.chunk or plugin.chunk
+        self.e_align = plugin.e_align
+        self._scratch = None                              # per-atom loc (int32, -1) and flag (bool) of chunk_topology
+        self._l1 = None
+        self.gx = None
+        self.n_captures = 0
+        self.log = open(k.log_path, "a", buffering=1) if k.log_path else None
+
+    def covers(self, elems):
+        return set(torch.unique(elems).tolist()) <= set(self.cols)
+
+    def layer1_cache(self, nl):
+        if not self.knobs.cache_layer1:
+            return None
+        if self._l1 is None or self._l1["rho"].numel() < nl:
+            self._l1 = None
+            self._l1 = self.fl.layer1_cache(nl)
+        return self._l1
+
+    def chunks(self, batch, elems, nl, nt):
+        """Receiver chunks [a, a + chunk) of the local atoms with their topology (receivers, then the senders
+        outside the chunk in ascending order; the reference's _topology_all, mliap_threepass.py:288-331)."""
+        if self._scratch is None or self._scratch[0].numel() < nt:
+            self._scratch = (torch.full((max(nt, 1),), -1, dtype=torch.int32, device=self.dev),
+                             torch.zeros(max(nt, 1), dtype=torch.bool, device=self.dev))
+        loc, flag = self._scratch
+        spec_all = self.fl.col2s[elems]
+        rp = batch.rowptr_host
+        out = []
+        for a in range(0, nl, self.chunk):
+            b = min(a + self.chunk, nl)
+            e0, e1 = int(rp[a]), int(rp[b])
+            nodes, ls = chunk_topology(a, b, e0, e1, batch.pair_j, loc, flag)
+            g = make_chunk(a, b, e0, e1, nodes, ls, batch.rowptr, spec_all)
+            g.rij, g.pair_i = batch.rij[e0:e1], batch.pair_i[e0:e1]
+            if self.knobs.check:
+                check_chunk(g, nt, self.fl.S)
+            out.append(g)
+        return out
+
+    def graph_executor(self, chunks, nt):
+        """The executor that replays the full chunks of this call (captured anew when a capacity is exceeded or
+        the layer-1 cache setting changed; mliap_threepass.py:390-431); None without full chunks or graphs."""
+        if not self.knobs.graphs:
+            return None
+        full = [g for g in chunks if g.nC == self.chunk]
+        if not full:
+            return None
+        n_max = max(g.n_nodes for g in full)
+        e_max = max(g.nE for g in full)
+        gx = self.gx
+        if gx is None or gx.cache_layer1 != self.knobs.cache_layer1 or not gx.fits(n_max, e_max, nt):
+            self.gx = gx = None
+            torch.cuda.empty_cache()
+            caps = chunk_graphs.capacities(n_max, e_max, nt, self.e_align, self.knobs.cap_margin)
+            gx = chunk_graphs.ChunkGraphExec(self.fl, self.chunk, *caps, "rij", self.knobs.cache_layer1,
+                                             exchange=True)
+            self.gx = gx
+            self.n_captures += 1
+            if self.log is not None:
+                self.log.write(json.dumps(dict(capture=dict(n_cap=caps[0], e_cap=caps[1], nt_cap=caps[2]))) + "\n")
+        gx.begin(chunks)
+        return gx
+
+    def evaluate(self, data, batch, elems, nl, nt, P, timings):
+        """The three passes of one call: returns per-atom energies eat (fp64 [nl], without e0 and shift) and the
+        pair forces dE/drij (fp32 [P, 3], receiver-grouped order)."""
+        stamp = _Stamps(timings)
+        chunks = self.chunks(batch, elems, nl, nt)
+        gx = self.graph_executor(chunks, nt)
+        call = _CallBuffers(self, nl, nt, P, gx)
+        eager = _EagerPasses(self.fl, call)
+        run = [gx if gx is not None and g.nC == self.chunk else eager for g in chunks]
+        stamp("A_topology")
+        for ex, g in zip(run, chunks):
+            ex.pass_a(g)
+        call.after_pass_a()
+        exchange_in_column_blocks(data.forward_exchange, call.H1, call.H1x, self.D1)
+        stamp("A")
+        call.before_pass_b()
+        for ex, g in zip(run, chunks):
+            ex.pass_b(g)
+        call.after_pass_b()
+        exchange_in_column_blocks(data.reverse_exchange, call.G1, call.G1r, self.D1)
+        stamp("B")
+        call.before_pass_c()
+        for ex, g in zip(run, chunks):
+            ex.pass_c(g)
+        if gx is not None:
+            gx.finish(chunks, call.PF)
+        stamp("C")
+        return call.eat, call.PF, len(chunks)
+
+
+class _Stamps:
+    """Wall time of each phase into `timings` (synchronising the device), or nothing when timings is None."""
+
+    def __init__(self, timings):
+        self.t, self.last = timings, time.perf_counter()
+        if timings is not None:
+            torch.cuda.synchronize()
+            self.last = time.perf_counter()
+
+    def __call__(self, name):
+        if self.t is None:
+            return
+        torch.cuda.synchronize()
+        now = time.perf_counter()
+        self.t[name] = now - self.last
+        self.last = now
 
 
 class ThreePassMLIAP(MLIAPUnified):
+    """The ML-IAP unified plugin (drop-in for mace_onegpu.mliap_threepass.ThreePassMLIAP).
+
+    model: a mace_onegpu.model.MaceModel (fp32); chunk: receivers per chunk; spline_grid: knots of the radial-weight
+    tables; node_bucket: kept for the reference's constructor (node counts are not bucketed here);
+    e_align: alignment of the graph executor's edge capacity; rebuild_config: constructor kwargs of the model's
+    class, stored with its state_dict so the pickled file holds a recipe instead of the module."""
+
     def __init__(self, model, chunk=16384, spline_grid=512, node_bucket=8192, e_align=65536, rebuild_config=None):
         super().__init__()
         self.model = model
@@ -75,220 +359,75 @@ class ThreePassMLIAP(MLIAPUnified):
         self.e_align = int(e_align)
         self.dtype = next(model.parameters()).dtype
         self.step = 0
-        # rebuild recipe (class, constructor kwargs, state_dict): the file then stores no module object and the
-        # model is constructed again on the first force call (mliap_threepass.py:172-202)
-        self._rebuild = None
+        self.profile = False            # per-pass wall times in last_timings (synchronises after every pass)
+        self.last_timings = None
+        self._recipe = None
         if rebuild_config is not None:
-            self._rebuild = (type(model), dict(rebuild_config),
-                             {k: v.detach().cpu() for k, v in model.state_dict().items()})
+            state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+            self._recipe = (type(model), dict(rebuild_config), state)
+        self._rt = None
 
-    # runtime objects (device tables, kernels' constants, graphs) are rebuilt after unpickling
+    @property
+    def n_captures(self):
+        """How many times the HIP graphs of full chunks were captured (0 without graphs)."""
+        return self._rt.n_captures if self._rt is not None else 0
+
+    # ------------------------------------------------------------------ pickling
     def __getstate__(self):
-        d = self.__dict__.copy()
-        for k in _RUNTIME:
-            d.pop(k, None)
-        if d.get("_rebuild") is not None:
-            d.pop("model", None)
-        return d
+        """Only the constructor's state travels in the model file; with a recipe the module itself stays out."""
+        state = {k: v for k, v in self.__dict__.items() if k not in ("_rt", "last_timings")}
+        if self._recipe is not None:
+            state.pop("model", None)
+        return state
+
+    def __setstate__(self, state):
+        self.__dict__.update(state)
+        self._rt = None
+        self.last_timings = None
 
     def _rebuild_model(self):
-        cls, cfg, sd = self._rebuild
-        m = cls(**cfg)
-        m.load_state_dict(sd, strict=True)
+        cls, kwargs, state = self._recipe
+        m = cls(**kwargs)
+        m.load_state_dict(state, strict=True)
         return m.to(self.dtype)
 
-    # ------------------------------------------------------------------ setup
-    def _setup(self, elems):
-        dev = elems.device if elems.is_cuda else torch.device("cuda")
-        self._dev = dev
+    def _runtime_for(self, elems):
+        rt = self._rt
+        if rt is not None and rt.covers(elems):
+            return rt
         if getattr(self, "model", None) is None:
             self.model = self._rebuild_model()
-        if os.environ.get("MACE3P_CHUNK"):
-            self.chunk = int(os.environ["MACE3P_CHUNK"])
-        self.model = self.model.to(dev).eval()
-        for p in self.model.parameters():
-            p.requires_grad_(False)
-        cols = sorted(int(c) for c in torch.unique(elems).tolist())
-        self._cols = cols
-        # MACE3P_ACE_L1=1 (default): layer 1 in the exact density-projection form (csrc/ace.hip)
-        ace = os.environ.get("MACE3P_ACE_L1", "1") == "1"
-        self._fl = fast_layers.FastLayers(self.model, cols, spline_grid=self.spline_grid, device=dev, ace_layer1=ace)
-        self.scale, self.shift = self._fl.scale, self._fl.shift
-        self._e0 = self._fl.e0
-        self._loc = None
-        self._flag = None
-        self._D1 = 4 * self.model.spec.C
-        self._fmax_abort = float(os.environ.get("MACE3P_FMAX_ABORT", "100.0"))
-        # MACE3P_CACHE_L1=1 (default): pass A keeps the layer-1 message and density of every local atom
-        # (8 KiB per atom) and pass C reuses them instead of recomputing layer 1
-        self._cache_l1 = os.environ.get("MACE3P_CACHE_L1", "1") == "1"
-        self._l1cache = None
-        self._use_graphs = os.environ.get("MACE3P_GRAPHS", "0") == "1"
-        self._gx = None
-        self._peak = 0.0
-        path = os.environ.get("MACE3P_LOG")
-        self._log = open(path, "a", buffering=1) if path else None
+        dev = elems.device if elems.is_cuda else torch.device("cuda")
+        self._rt = _Runtime(self, elems.to(dev), dev)
+        return self._rt
 
-    def _prepare_graphs(self, graphs, nt):
-        """A captured executor that fits every full chunk of this call (recaptured when a capacity is exceeded);
-        None without full chunks (mliap_threepass.py:390-431)."""
-        full = [g for g in graphs if g.nC == self.chunk]
-        if not full:
-            return None
-        n_max = max(g.n_nodes for g in full)
-        e_max = max(g.nE for g in full)
-        gx = self._gx
-        if gx is None or gx.cache_layer1 != self._cache_l1 or not gx.fits(n_max, e_max, nt):
-            self._gx = gx = None
-            torch.cuda.empty_cache()
-            margin = float(os.environ.get("MACE3P_CAP_MARGIN", "1.25"))
-            n_cap, e_cap, nt_cap = chunk_graphs.capacities(n_max, e_max, nt, self.e_align, margin)
-            gx = chunk_graphs.ChunkGraphExec(self._fl, self.chunk, n_cap, e_cap, nt_cap, "rij", self._cache_l1,
-                                             exchange=True)
-            self._gx = gx
-            self.n_captures = getattr(self, "n_captures", 0) + 1
-            if self._log is not None:
-                self._log.write(json.dumps(dict(capture=dict(n_cap=n_cap, e_cap=e_cap, nt_cap=nt_cap))) + "\n")
-        gx.begin(graphs)
-        return gx
-
-    def _topology_all(self, bounds, rp_cpu, pi, pj, nl, nt):
-        """{(a, b): (nodes int32, local sender index int32 [nE])} for every receiver chunk, identical to
-        ThreePassMLIAP._topology chunk by chunk (mliap_threepass.py:288-310, :344-388)."""
-        dev = self._dev
-        if self._loc is None or self._loc.numel() < nt:
-            self._loc = torch.full((max(nt, 1),), -1, dtype=torch.int32, device=dev)
-            self._flag = torch.zeros(max(nt, 1), dtype=torch.bool, device=dev)
-        out = {}
-        for a, b in bounds:
-            e0, e1 = int(rp_cpu[a]), int(rp_cpu[b])
-            out[(a, b)] = chunk_topology(a, b, e0, e1, pj, self._loc, self._flag)
-        return out
-
-    # ------------------------------------------------------------------ LAMMPS entry point
+    # ------------------------------------------------------------------ LAMMPS entry points
     def compute_forces(self, data):
+        """Per-atom energies into data.eatoms, the total into data.energy and dE/drij (fp64 [npairs, 3]) through
+        data.update_pair_forces_gpu; nothing happens for nlocal == 0 or npairs <= 1."""
         nl, nt, P = int(data.nlocal), int(data.ntotal), int(data.npairs)
         if nl == 0 or P <= 1:
             return
-        t_start = time.perf_counter()
-        # int32 neighbour-slot guard of the LAMMPS/Kokkos neighbour list (mliap_threepass.py:450-461)
-        skin = float(os.environ.get("MACE3P_SKIN", "2.0"))
-        rmax = 2.0 * self.rcutfac
-        est_slots = P * ((rmax + skin) / rmax) ** 3
-        if est_slots > 0.95 * 2 ** 31 and os.environ.get("MACE3P_ALLOW_HUGE", "0") != "1":
-            raise RuntimeError(f"ThreePassMLIAP guard: nlocal={nl:,}, pairs={P:,} -> estimated LAMMPS neighbour slots "
-                               f"{est_slots:.3e} is close to the 2^31 int32 limit of the Kokkos neighbour list "
-                               f"(skin {skin} A). Use fewer atoms per GPU, a smaller skin, or more GPUs.")
+        t_call = time.perf_counter()
+        neighbour_slot_guard(nl, P, self.rcutfac)
         elems = torch.as_tensor(data.elems).long()
-        if not hasattr(self, "_fl") or not set(torch.unique(elems).tolist()) <= set(self._cols):
-            self._setup(elems)
+        rt = self._runtime_for(elems)
         self.step += 1
-        dev, fl, D1 = self._dev, self._fl, self._D1
-        elems = elems.to(dev)
-        pi = torch.as_tensor(data.pair_i).to(dev).int()
-        pj = torch.as_tensor(data.pair_j).to(dev).int()
-        rij = torch.as_tensor(data.rij).to(dev).double()
-        order = None
-        if not bool((pi[1:] >= pi[:-1]).all()):
-            order = torch.argsort(pi, stable=True)
-            pi, pj, rij = pi[order], pj[order], rij[order]
-        pi, pj, rij = pi.contiguous(), pj.contiguous(), rij.contiguous()
-        rp = torch.searchsorted(pi, torch.arange(nl + 1, device=dev, dtype=pi.dtype))
-        rp_cpu = rp.cpu().numpy()
-        C = self.chunk
-        bounds = [(a, min(a + C, nl)) for a in range(0, nl, C)]
-        node_spec_all = fl.col2s[elems]
-        t = {}
-        t0 = time.perf_counter()
-        topo = self._topology_all(bounds, rp_cpu, pi, pj, nl, nt)
-        graphs = []
-        for a, b in bounds:
-            e0, e1 = int(rp_cpu[a]), int(rp_cpu[b])
-            g = make_chunk(a, b, e0, e1, topo[(a, b)][0], topo[(a, b)][1], rp, node_spec_all)
-            g.rij, g.pair_i = rij[e0:e1], pi[e0:e1]
-            graphs.append(g)
-        gx = self._prepare_graphs(graphs, nt) if self._use_graphs else None
-        torch.cuda.synchronize()
-        t["A_topology"] = time.perf_counter() - t0
-        PF = torch.zeros(P, 3, dtype=torch.float32, device=dev)
-        # ---------------- pass A
-        t0 = time.perf_counter()
-        cache = None
-        if gx is not None:      # the executor's static buffers: its graphs read and write them in place
-            H1, eat = gx.H1[:nt], gx.eat[:nl]
-            H1.zero_()
-            cache = gx.cache()
-        else:
-            H1 = torch.zeros(nt, D1, dtype=torch.float32, device=dev)
-            eat = torch.zeros(nl, dtype=torch.float64, device=dev)
-            if self._cache_l1:
-                if self._l1cache is None or self._l1cache["rho"].numel() < nl:
-                    self._l1cache = fl.layer1_cache(nl)
-                cache = self._l1cache
-        for g in graphs:
-            if gx is not None and g.nC == C:
-                gx.pass_a(g)
-            else:
-                fl.pass_a(g, H1, cache)
-        H1x = gx.H1x[:nt] if gx is not None else torch.empty_like(H1)
-        _exchange(data.forward_exchange, H1, H1x, D1)
-        del H1
-        torch.cuda.synchronize()
-        t["A"] = time.perf_counter() - t0
-        # ---------------- pass B
-        t0 = time.perf_counter()
-        if gx is not None:
-            G1 = gx.G1[:nt]
-            G1.zero_()
-            eat.zero_()
-        else:
-            G1 = torch.zeros_like(H1x)
-        for g in graphs:
-            if gx is not None and g.nC == C:
-                gx.pass_b(g)
-            else:
-                fl.pass_b(g, H1x, G1, PF, eat)
-        H1c = H1x if cache is not None else None       # pass C reads h1 from H1x only with the layer-1 cache
-        del H1x
-        G1r = gx.G1r[:nt] if gx is not None else torch.empty_like(G1)
-        _exchange(data.reverse_exchange, G1, G1r, D1)
-        del G1
-        torch.cuda.synchronize()
-        t["B"] = time.perf_counter() - t0
-        # ---------------- pass C
-        t0 = time.perf_counter()
-        for g in graphs:
-            if gx is not None and g.nC == C:
-                gx.pass_c(g)
-            elif cache is None:
-                fl.pass_c(g, G1r, PF, eat)
-            else:
-                fl.pass_c(g, G1r, PF, eat, H1c, cache)
-        if gx is not None:
-            gx.finish(graphs, PF)
-        del G1r, H1c
-        torch.cuda.synchronize()
-        t["C"] = time.perf_counter() - t0
-        eat = eat + self._e0[elems[:nl]] + self.shift
-        PF = PF.double()
-        if order is not None:
-            out = torch.empty_like(PF)
-            out[order] = PF
-            PF = out
-        # non-finite / absurd output guard (mliap_threepass.py:595-601)
-        fmax = float(PF.abs().max()) if PF.numel() else 0.0
-        if not (bool(torch.isfinite(eat).all()) and fmax == fmax and fmax < self._fmax_abort):
-            raise RuntimeError(f"ThreePassMLIAP guard: non-finite or absurd output at call {self.step} "
-                               f"(max |pair force| = {fmax:.3e} eV/A, limit {self._fmax_abort:g}); aborting before LAMMPS "
-                               f"integrates it. The model is probably extrapolating (check the trajectory / training data).")
+        elems = elems.to(rt.dev)
+        timings = {} if (self.profile or rt.log is not None) else None
+        batch = _PairBatch(data, nl, nt, rt.dev, rt.knobs.check)
+        eat, PF, n_chunks = rt.evaluate(data, batch, elems, nl, nt, P, timings)
+        eat = eat + rt.e0[elems[:nl]] + rt.shift
+        PF = batch.restore(PF.double())
+        output_guard(eat, PF, rt.knobs.fmax_abort, self.step)
         torch.as_tensor(data.eatoms).copy_(eat)
         data.energy = float(eat.sum())
         data.update_pair_forces_gpu(PF)
-        self.last_timings = t
-        if self._log is not None:
-            self._log.write(json.dumps(dict(step=self.step, nlocal=nl, ntotal=nt, npairs=P, chunks=len(bounds),
-                                            sorted_pairs=order is None, t_total=time.perf_counter() - t_start,
-                                            **t)) + "\n")
+        self.last_timings = timings
+        if rt.log is not None:
+            rt.log.write(json.dumps(dict(step=self.step, nlocal=nl, ntotal=nt, npairs=P, chunks=n_chunks,
+                                         sorted_pairs=batch.perm is None, graphs=rt.gx is not None,
+                                         t_total=time.perf_counter() - t_call, **timings)) + "\n")
 
     def compute_descriptors(self, data):
         pass

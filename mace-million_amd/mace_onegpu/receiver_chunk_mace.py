@@ -10,6 +10,7 @@ Mirrors mace_onegpu/receiver_chunk_mace.py of the reference:
     are the fp64 minimum images of the sorted positions; forces F = -dE/dx in fp64.
 """
 import ctypes
+import os
 import time
 
 import numpy as np
@@ -122,6 +123,44 @@ def chunk_topology(a, b, e0, e1, pj, loc, flag):
     return nodes, ls
 
 
+def check_chunk(g, n_atoms, n_species=None):
+    """Host-side range check of one chunk's index arrays before its kernels dereference them (opt-in:
+    MACE3P_CHECK=1 in ThreePassMLIAP, check=True in ReceiverChunkMACE; a few device-to-host reads per chunk).
+    Raises ValueError naming the array: the receiver CSR (monotone, from 0 to nE), local senders in
+    [0, n_nodes), node rows in [0, n_atoms) with the receivers a..b-1 first, species in [0, n_species), and the
+    receiver of every edge inside the chunk."""
+    def span(t):
+        t = t.reshape(-1)
+        return (int(t.min()), int(t.max())) if t.numel() else (0, -1)
+    nC, nE, n = g.nC, g.nE, g.n_nodes
+    rp = g.rowptr
+    if rp.numel() != nC + 1:
+        raise ValueError(f"chunk [{g.a}, {g.b}): rowptr has {rp.numel()} entries, expected {nC + 1}")
+    if int(rp[0]) != 0 or int(rp[-1]) != nE or (nC > 0 and bool((rp[1:] < rp[:-1]).any())):
+        raise ValueError(f"chunk [{g.a}, {g.b}): rowptr is not a monotone CSR from 0 to nE = {nE}")
+    lo, hi = span(g.ls[:nE])
+    if g.ls.numel() < nE or lo < 0 or hi >= n:
+        raise ValueError(f"chunk [{g.a}, {g.b}): local senders span [{lo}, {hi}], outside [0, {n})")
+    lo, hi = span(g.nodes)
+    if g.nodes.numel() != n or lo < 0 or hi >= n_atoms:
+        raise ValueError(f"chunk [{g.a}, {g.b}): node rows span [{lo}, {hi}], outside [0, {n_atoms})")
+    if not torch.equal(g.nodes[:nC].long().cpu(), torch.arange(g.a, g.b)):
+        raise ValueError(f"chunk [{g.a}, {g.b}): the first nodes are not the receivers a..b-1")
+    lo, hi = span(g.node_spec)
+    if g.node_spec.numel() != n or lo < 0 or (n_species is not None and hi >= n_species):
+        raise ValueError(f"chunk [{g.a}, {g.b}): node species span [{lo}, {hi}] (species not in the model's "
+                         f"present columns?)")
+    if g.rij is not None:
+        if g.rij.shape[0] < nE or g.pair_i.numel() < nE:
+            raise ValueError(f"chunk [{g.a}, {g.b}): fewer pair vectors or receivers than edges")
+        recv = g.pair_i[:nE].long() - g.a
+    else:
+        recv = g.recv_local[:nE].long()
+    lo, hi = span(recv)
+    if lo < 0 or hi >= nC:
+        raise ValueError(f"chunk [{g.a}, {g.b}): edge receivers span [{lo}, {hi}] (chunk-local), outside [0, {nC})")
+
+
 def make_chunk(a, b, e0, e1, nodes, ls, rowptr_full, node_spec_all):
     g = ChunkGraph()
     g.a, g.b, g.e0, g.e1 = a, b, e0, e1
@@ -138,8 +177,10 @@ class ReceiverChunkMACE:
     """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
 
     def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True, use_graphs=False,
-                 e_align=65536, ace_layer1=True):
+                 e_align=65536, ace_layer1=True, check=None):
         self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
+        # host-side range check of every chunk's index arrays before its kernels run (check_chunk)
+        self.check = (os.environ.get("MACE3P_CHECK", "0") == "1") if check is None else bool(check)
         self.ace_layer1 = bool(ace_layer1)       # layer 1 in the exact density-projection form (csrc/ace.hip)
         self.dev = torch.device(device)
         self.fl = None
@@ -188,6 +229,12 @@ class ReceiverChunkMACE:
             out.append(g)
         return out
 
+    def _checked(self, graphs, sysm, fl):
+        if self.check:
+            for g in graphs:
+                check_chunk(g, sysm.N, fl.S)
+        return graphs
+
     def _graph_exec(self, fl, sysm, graphs):
         """The HIP-graph executor of this call's full chunks, their topology loaded (a new executor -- new
         captures -- when the box changes or a capacity is exceeded); None without full chunks."""
@@ -216,7 +263,7 @@ class ReceiverChunkMACE:
         """Returns (E float, eat fp64 [N], F fp64 [N, 3], PF fp32 [E, 3]) in the sorted index space."""
         fl = self._layers(sysm)
         dev, N = self.dev, sysm.N
-        graphs = graphs if graphs is not None else self.graphs(sysm)
+        graphs = self._checked(graphs if graphs is not None else self.graphs(sysm), sysm, fl)
         E = sum(g.nE for g in graphs)
         t = {}
         sync = torch.cuda.synchronize if timings is not None else (lambda: None)   # pass timings only on request

@@ -13,10 +13,20 @@ What it restates (reference file:line):
     TG = h dW/dr) and the cubic-Hermite lookup of spline_w._w_fwd (spline_w.py:18-50, clamp to M - 1 - 1e-4).
 The TP and the symmetric contraction are evaluated densely from the coupling tensors (einsum), independently of
 the sparse term lists that the GPU kernels are generated from.
-Pinned by: rotation/translation/permutation invariance of E and covariance of F (fails for a wrong coupling
-sign, a transposed coupling or a wrong SH), finite differences of E against F, three-pass == full graph and chunk
-invariance (the reference's own criteria, test_threepass.py:66-88), the SH against scipy.special, the coupling
-tensors' equivariance, and the symmetric-contraction basis against the dimension of the equivariant space.
+Pinned by (tests/test_oracle.py, tests/test_oracle_conventions.py, tests/test_o3.py):
+  * rotation/translation/permutation invariance of E and covariance of F (fails for a wrong coupling sign, a
+    transposed coupling or a wrong SH), finite differences of E against F, three-pass == full graph and chunk
+    invariance (the reference's own criteria, test_threepass.py:66-88);
+  * the SH against scipy.special, the coupling tensors' equivariance, the symmetric-contraction basis against the
+    dimension of the equivariant space;
+  * bessel: orthonormality on [0, r_max] with weight r^2 (quadrature); poly_cutoff: the unique degree-(p+2)
+    polynomial with f(0) = 1 and f = f' = f'' = 0 at r_max; silu_n: Gauss-Hermite quadrature;
+  * the e3nn normalisations of radial_mlp, per_l_linear, multi_source_linear, skip_tp, node_embedding, the
+    readouts, density_z and every channelwise-TP path: unit second moment for unit-variance inputs (Monte Carlo);
+  * the density normalisation: the closed forms rho = 0 (w = 0) and rho = sum f_cut (saturated tanh);
+  * E_i = e0 + shift + scale (R1 + R2): affine in scale / shift / E0, three-pass and full graph alike.
+Parity unpinned: absolute values against mace-torch itself (not installed); the basis of the real harmonics
+(z-polar here) and of the symmetric contraction are reparametrisations of random-init weights.
 """
 import math
 
@@ -69,15 +79,31 @@ def poly_cutoff(r, r_max, p):
     return env * (x < 1.0).to(r.dtype)
 
 
+def silu_n(z):
+    """e3nn normalize2mom(silu): silu scaled to unit second moment under z ~ N(0, 1)."""
+    return silu_norm() * torch.nn.functional.silu(z)
+
+
 def radial_mlp(B, Ws):
-    """e3nn FullyConnectedNet: hidden h <- silu_n(h @ W / sqrt(fan_in)); last layer linear."""
+    """e3nn FullyConnectedNet (mace's conv_tp_weights, receiver_chunk_mace.py:230-234 via
+    fast_layers.py:150-156): hidden h <- silu_n(h @ W / sqrt(fan_in)); the last layer is linear."""
     h = B
-    cst = silu_norm()
     for j, W in enumerate(Ws):
         h = h @ W / math.sqrt(W.shape[0])
         if j < len(Ws) - 1:
-            h = cst * torch.nn.functional.silu(h)
+            h = silu_n(h)
     return h
+
+
+def density_z(B, w):
+    """Pre-activation of mace's density_fn (a one-layer FullyConnectedNet, fast_layers.py:179-185):
+    z = B @ w / sqrt(n_bessel); B [E, nb], w [nb, 1] -> [E]."""
+    return (B @ w / math.sqrt(B.shape[1]))[:, 0]
+
+
+def edge_density(B, w, f):
+    """Edge density d_e = tanh(z_e^2) * f_cut(r_e) (fast_layers.py:181-183, cutoff branch :190-192)."""
+    return torch.tanh(density_z(B, w) ** 2) * f
 
 
 # ----------------------------------------------------------------------------- equivariant operations
@@ -142,9 +168,47 @@ def symmetric_contraction(x, species, weights, paths, out_ls, in_ls, coupling):
 
 
 def per_l_linear(x, ls, Wl, C):
-    """Equivariant linear, one weight [C, C] per irrep in ls (in order): x [n, comps, C]."""
+    """e3nn Linear between equal irreps (one weight [C, C] per irrep l in ls, in order; x [n, comps, C]):
+    y = x_l @ W_l / sqrt(C) (mace's linear_up, products[k].linear)."""
     offs, _ = comp_offsets(ls)
     return torch.cat([x[:, o:o + 2 * l + 1, :] @ Wl[i] / math.sqrt(C) for i, (o, l) in enumerate(zip(offs, ls))], 1)
+
+
+def multi_source_linear(blocks, Ws):
+    """e3nn Linear into one output irrep fed by several input segments of that irrep (layer 2's interaction
+    linear, mid irreps -> target): y = sum_j x_j @ W_j / sqrt(C * n_src); blocks [n, 2l+1, C] each."""
+    fan_in = blocks[0].shape[-1] * len(blocks)
+    acc = 0
+    for x, W in zip(blocks, Ws):
+        acc = acc + x @ W
+    return acc / math.sqrt(fan_in)
+
+
+def node_embedding(attrs, emb):
+    """mace LinearNodeEmbeddingBlock, an e3nn Linear n_el x 0e -> C x 0e: attrs [n, n_el] @ emb / sqrt(n_el)."""
+    return attrs @ emb / math.sqrt(emb.shape[0])
+
+
+def skip_tp(x, y, W):
+    """e3nn FullyConnectedTensorProduct(x irreps, n_el x 0e, x irreps) (mace's skip_tp, fast_layers.py:41-105):
+    out[n, m, d] = sum_{c, s} x[n, m, c] y[n, s] W[c, s, d] / sqrt(C * n_el).  y is either the node attributes
+    [n, n_el] (float) or, for one-hot attributes, the species index per node [n] (long)."""
+    C, ne = W.shape[0], W.shape[1]
+    if y.dtype == torch.long:
+        Wn = W[:, y, :].permute(1, 0, 2)                       # [n, C_in, C_out]
+    else:
+        Wn = torch.einsum("ns,csd->ncd", y, W)
+    return torch.einsum("nmc,ncd->nmd", x, Wn) / math.sqrt(C * ne)
+
+
+def readout_linear(h0, w):
+    """mace LinearReadoutBlock (layer 1): h[0e] @ w / sqrt(C)."""
+    return h0 @ w / math.sqrt(w.shape[0])
+
+
+def readout_mlp(h0, W1, w2):
+    """mace NonLinearReadoutBlock (layer 2): silu_n(h @ W1 / sqrt(C)) @ w2 / sqrt(n_hidden)."""
+    return silu_n(h0 @ W1 / math.sqrt(W1.shape[0])) @ w2 / math.sqrt(w2.shape[0])
 
 
 # ----------------------------------------------------------------------------- model access
@@ -223,43 +287,44 @@ def _weights_density(m, k, r, B, f, tables, pair):
         W = radial_mlp(B, m.radial_W(k)) * f[:, None]
     else:
         W = tables.lookup(k, r, pair)
-    d = torch.tanh((B @ m.P[f"i{k}_dens"] / math.sqrt(m.nb)) ** 2)[:, 0] * f
-    return W, d
+    return W, edge_density(B, m.P[f"i{k}_dens"], f)
 
 
-def layer1(m, spec_nodes, nC, send, recv, vec, tables=None, pair=None):
-    """h1 [nC, 4, C] of the receivers (local nodes 0..nC-1); spec_nodes: model element index per local node."""
+def layer1_message(m, spec_nodes, nC, send, recv, vec, tables=None, pair=None):
+    """Layer-1 interaction (RealAgnosticDensityInteractionBlock, fast_layers.py:168-200) up to the message
+    before skip_tp: linear(sum_e TP(W_e, X[send_e], Y_e)) / (rho + 1) [nC, 16, C], rho = sum_e d_e."""
     C = m.C
     r, Y, B, f = _edge(m, vec)
     W, d = _weights_density(m, 0, r, B, f, tables, pair)
     W = W.reshape(-1, m.tp1["nW"], C)
     onehot = torch.nn.functional.one_hot(spec_nodes, m.ne).to(F64)
-    X = (onehot @ m.P["emb"] / math.sqrt(m.ne)) @ m.P["i0_up"][0] / math.sqrt(C)
-    mji = channelwise_tp(W, X[:, None, :], Y, send, m.tp1["paths"], m.tp1["in_ls"], m.coupling)
+    X = per_l_linear(node_embedding(onehot, m.P["emb"])[:, None, :], [0], m.P["i0_up"], C)
+    mji = channelwise_tp(W, X, Y, send, m.tp1["paths"], m.tp1["in_ls"], m.coupling)
     A = scatter_sum(mji, recv, nC)
     rho = scatter_sum(d, recv, nC)
-    M = per_l_linear(A, m.tp1["mid_ls"], m.P["i0_lin"], C) / (rho[:, None, None] + 1)
+    return per_l_linear(A, m.tp1["mid_ls"], m.P["i0_lin"], C) / (rho[:, None, None] + 1)
+
+
+def layer1(m, spec_nodes, nC, send, recv, vec, tables=None, pair=None):
+    """h1 [nC, 4, C] of the receivers (local nodes 0..nC-1); spec_nodes: model element index per local node."""
+    M = layer1_message(m, spec_nodes, nC, send, recv, vec, tables, pair)
     s = spec_nodes[:nC]
     offs, _ = comp_offsets(m.tp1["mid_ls"])
-    Ms = []
-    for i, (o, l) in enumerate(zip(offs, m.tp1["mid_ls"])):
-        Wsk = m.P["i0_skip"][i][:, s, :].permute(1, 0, 2)       # [n, C_in, C_out]
-        Ms.append(torch.einsum("nmc,ncd->nmd", M[:, o:o + 2 * l + 1, :], Wsk) / math.sqrt(C * m.ne))
-    M = torch.cat(Ms, 1)
+    M = torch.cat([skip_tp(M[:, o:o + 2 * l + 1, :], s, m.P["i0_skip"][i])
+                   for i, (o, l) in enumerate(zip(offs, m.tp1["mid_ls"]))], 1)
     Bsc = symmetric_contraction(M, s, m.sym_weights(0, (0, 1)), m.sc1, [0, 1], [0, 1, 2, 3], m.coupling)
-    return per_l_linear(Bsc, [0, 1], m.P["p0_lin"], C)
+    return per_l_linear(Bsc, [0, 1], m.P["p0_lin"], m.C)
 
 
 def readout1(m, h1):
-    return h1[:, 0, :] @ m.P["r0"] / math.sqrt(m.C)
+    return readout_linear(h1[:, 0, :], m.P["r0"])
 
 
 def layer2_energy(m, spec_nodes, nC, send, recv, vec, h1_nodes, tables=None, pair=None):
     """Per-receiver layer-2 energy R2(h2) [nC]; h1_nodes [n_nodes, 4, C] for every local node."""
     C = m.C
     s = spec_nodes[:nC]
-    Wsk = m.P["i1_skip"][:, s, :].permute(1, 0, 2)
-    sc = torch.einsum("nc,ncd->nd", h1_nodes[:nC, 0, :], Wsk) / math.sqrt(C * m.ne)
+    sc = skip_tp(h1_nodes[:nC, 0:1, :], s, m.P["i1_skip"])[:, 0, :]
     X = per_l_linear(h1_nodes, [0, 1], m.P["i1_up"], C)
     r, Y, B, f = _edge(m, vec)
     W, d = _weights_density(m, 1, r, B, f, tables, pair)
@@ -272,15 +337,12 @@ def layer2_energy(m, spec_nodes, nC, send, recv, vec, h1_nodes, tables=None, pai
     for l in [0, 1, 2, 3]:
         src = m.lin2_src[l]
         Wl = m.P[f"i1_lin_l{l}"]
-        acc = 0
-        for j, w in enumerate(src):
-            acc = acc + A[:, mo[w]:mo[w] + 2 * l + 1, :] @ Wl[j]
-        outs.append(acc / math.sqrt(C * len(src)))
+        outs.append(multi_source_linear([A[:, mo[w]:mo[w] + 2 * l + 1, :] for w in src],
+                                        [Wl[j] for j in range(len(src))]))
     M2 = torch.cat(outs, 1) / (rho[:, None, None] + 1)
     B2 = symmetric_contraction(M2, s, m.sym_weights(1, (0,)), m.sc2, [0], [0, 1, 2, 3], m.coupling)
-    h2 = B2[:, 0, :] @ m.P["p1_lin"][0] / math.sqrt(C) + sc
-    z = h2 @ m.P["r1_w1"] / math.sqrt(C)
-    return (silu_norm() * torch.nn.functional.silu(z)) @ m.P["r1_w2"] / math.sqrt(m.P["r1_w2"].shape[0])
+    h2 = per_l_linear(B2, [0], m.P["p1_lin"], C)[:, 0, :] + sc
+    return readout_mlp(h2, m.P["r1_w1"], m.P["r1_w2"])
 
 
 # ----------------------------------------------------------------------------- full graph

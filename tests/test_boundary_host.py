@@ -4,7 +4,7 @@ import pytest
 import torch
 
 from mace_onegpu import mliap_threepass
-from mace_onegpu.mliap_threepass import ThreePassMLIAP, _exchange
+from mace_onegpu.mliap_threepass import ThreePassMLIAP, exchange_in_column_blocks
 
 
 class _Data:
@@ -47,7 +47,7 @@ def test_int32_slot_guard(plugin, monkeypatch):
 def test_exchange_column_split(monkeypatch):
     """ntotal * D >= 2^31 elements: the exchange is called on column blocks that each stay below the limit,
     and the blocks reassemble the full result."""
-    monkeypatch.setattr(mliap_threepass, "_INT_MAX", 1000)
+    monkeypatch.setattr(mliap_threepass, "INT32_ELEMENTS", 1000)
     calls = []
 
     def fn(src, dst, D):
@@ -57,21 +57,20 @@ def test_exchange_column_split(monkeypatch):
 
     src = torch.arange(40 * 64, dtype=torch.float32).view(40, 64)
     dst = torch.empty_like(src)
-    _exchange(fn, src, dst, 64)
+    exchange_in_column_blocks(fn, src, dst, 64)
     assert torch.equal(dst, 2 * src)
     assert len(calls) > 1 and sum(calls) == 64
     calls.clear()
     small = torch.ones(3, 8)
     out = torch.empty_like(small)
-    _exchange(fn, small, out, 8)                       # below the limit: one call on the whole array
+    exchange_in_column_blocks(fn, small, out, 8)                       # below the limit: one call on the whole array
     assert calls == [8] and torch.equal(out, 2 * small)
 
 
 def test_pickle_drops_runtime_state(model):
     import pickle
     tp = ThreePassMLIAP(model, chunk=32)
-    for k in mliap_threepass._RUNTIME:
-        setattr(tp, k, object())
+    tp._rt = object()                                  # stands in for the device runtime of a used plugin
     back = pickle.loads(pickle.dumps(tp))
-    assert not any(hasattr(back, k) for k in mliap_threepass._RUNTIME)
+    assert back._rt is None and back.step == 0
     assert back.chunk == 32 and back.rcutfac == 0.5 * model.spec.r_max

@@ -77,3 +77,39 @@ def test_edge_geometry_against_fp64(x_from_spec):
     assert torch.equal(pki[:, 1].long(), row)
     assert torch.equal(pki[:, 2].long(), xsrc)
     assert torch.equal(e_recv.long(), recv)
+
+
+@pytest.mark.parametrize("M", [512, 4096, 8192])
+def test_spline_interval_stays_inside_the_table(M):
+    """Lengths at the top of the table and beyond r_max land in the last interval (k = M - 2, t in [0, 1]) for
+    every knot count: the fp32 clamp M - 1 - 1e-4 rounds to M - 1 for M >= 4096, and the interval index is clamped
+    separately so that no row points past the n_tab (M - 1) intervals of the table."""
+    from mace_onegpu._lib import K, stream
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    S, nb, p, r_lo, r_max = 1, 8, 5, 0.5, 6.0
+    h = (r_max - r_lo) / (M - 1)
+    r = torch.tensor([r_max - 0.5 * h, r_max - 1e-6, r_max, r_max + 0.3, 7.5, r_lo + 0.25 * h, 0.3],
+                     dtype=torch.float64)
+    E = r.numel()
+    print(f"case M={M}: {E} edges", flush=True)
+    rij = torch.stack([r, torch.zeros_like(r), torch.zeros_like(r)], 1)
+    dev = "cuda"
+    i32 = dict(dtype=torch.int32, device=dev)
+    e_u = torch.empty(E, 4, device=dev)
+    e_pk = torch.empty(E, 4, device=dev)
+    e_recv = torch.empty(E, **i32)
+    e_dd = torch.empty(E, device=dev)
+    dens_w = (ctypes.c_float * nb)(*([0.1] * nb))
+    K.mm_edge_geom_rij(E, rij.to(dev), torch.zeros(E, **i32), 0, torch.zeros(E, **i32), torch.zeros(1, **i32), S,
+                       torch.zeros(1, **i32), dens_w, nb, r_max, p, M, r_lo, 1.0 / h, 0, e_u, None, e_pk, e_recv,
+                       e_dd, stream())
+    torch.cuda.synchronize()
+    pk = e_pk.cpu()
+    row = pk.view(torch.int32)[:, 1].long()
+    t = pk[:, 0].double()
+    print(f"  rows {row.tolist()} t {[round(float(x), 4) for x in t]}", flush=True)
+    assert int(row.max()) <= M - 2 and int(row.min()) >= 0
+    assert bool(((t >= 0) & (t <= 1)).all())
+    assert row[:5].tolist() == [M - 2] * 5                        # r >= r_max - h/2: the last interval
+    assert row[5:].tolist() == [0, 0]                             # r <= r_lo + h/4: the first interval
+    assert float(t[6]) == 0.0                                     # below r_lo: clamped to the first knot

@@ -57,7 +57,7 @@ def test_mliap_graphs_match_eager(model, water_sys, cache_l1, monkeypatch):
         d1 = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True, shuffle_pairs_seed=shuffle)
         graphed.compute_forces(d1)
         torch.cuda.synchronize()
-        assert graphed._gx is not None and graphed._gx.n_replays == 12 * (call + 1)
+        assert graphed._rt.gx is not None and graphed._rt.gx.n_replays == 12 * (call + 1)
         _close(d1.energy, d1.pair_forces, d1.eatoms, d0.energy, d0.pair_forces, d0.eatoms, s.N, f"call {call}")
     assert graphed.n_captures == 1
 

@@ -1,0 +1,207 @@
+"""The remaining production paths against the fp64 oracle on the GPU (marked gpu): non-identity energy
+bookkeeping (scale, shift, per-species E0), the HIP-graph executor, the unpickled model file, and the MD driver
+(skin list, per-step filter, chunk templates, reverse-pair force sums, rebuilds), plus full-size properties of
+configuration 5 (1,029,000 atoms).
+
+Bars (as in test_gpu_parity.py): energies within 1e-5 eV/atom, forces within 1e-3 eV/A and within 1e-4 of
+max|F| against the exact fp64 oracle (fp32 arithmetic + 512-knot tables).  Reference criteria:
+mliap_threepass.py:241-248, 550, 578, 589 (scale / shift / E0), :390-431 (graphs), scripts/make_threepass_model.py
+(model file), graphed_three_pass.py:245-334 and tests/gpu/test_threepass.py:66-94 (MD shape and tolerances).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SCALE, SHIFT = 1.7, -0.35
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    return "cuda"
+
+
+@pytest.fixture(scope="module")
+def scaled_model():
+    """The seed-0 model with scale 1.7, shift -0.35 and a distinct E0 per element."""
+    from mace_onegpu import model as mm
+    m = mm.MaceModel(mm.MaceSpec(scale=SCALE, shift=SHIFT), seed=0)
+    m.e0.copy_(torch.linspace(-3.0, 2.0, m.spec.num_elements, dtype=torch.float64))
+    return m
+
+
+@pytest.fixture(scope="module")
+def scaled_ref(scaled_model):
+    from mace_onegpu import o3
+    from oracle import mace_ref
+    return mace_ref.RefModel(scaled_model, o3.coupling)
+
+
+@pytest.fixture(scope="module")
+def water(dev):
+    from mace_onegpu import systems
+    from mace_onegpu.receiver_chunk_mace import System
+    pos, box, Z = systems.water_box(64, seed=0)
+    s = System(pos, box, Z - 1, 6.0, dev)
+    s.build_neighbors()
+    return s
+
+
+def _oracle(ref, pos, box, spec, NN, send, chunk=192):
+    from oracle import mace_ref
+    recv = np.repeat(np.arange(len(pos)), NN)
+    return mace_ref.three_pass(ref, pos, box, spec, recv, send, chunk=chunk)
+
+
+def _oracle_sys(ref, s, chunk=192):
+    return _oracle(ref, s.pos.cpu().numpy(), s.box, s.spidx.cpu().numpy(), s.NN.cpu().numpy(),
+                   s.send.cpu().numpy(), chunk)
+
+
+def _check(what, E, eat, F, ref, N, rel=1e-4):
+    E0, e0, F0 = ref[0], ref[1], ref[2]
+    dE = abs(E - E0) / N
+    de = float((eat.cpu() - e0).abs().max())
+    dF = float((F.cpu() - F0).abs().max())
+    Fm = float(F0.abs().max())
+    _say(f"  {what}: E {E:.8f} (oracle {E0:.8f}) |dE|/N={dE:.2e} max|de_i|={de:.2e} max|dF|={dF:.2e} "
+         f"(max|F|={Fm:.3e}, rel {dF / Fm:.2e})")
+    assert dE < 1e-5 and de < 1e-5
+    assert dF < 1e-3 and dF < rel * Fm
+
+
+# ----------------------------------------------------------------------------- energy bookkeeping
+def test_scale_shift_e0_mliap_and_standalone(dev, scaled_model, scaled_ref, water):
+    """ThreePassMLIAP (ghosts, unsorted pairs) and ReceiverChunkMACE with scale != 1, shift != 0 and per-species
+    E0 against the oracle: the scale enters both readouts and the G1 chain, shift and E0 the per-atom energies."""
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
+    s = water
+    ref = _oracle_sys(scaled_ref, s)
+    _say("case scale/shift/E0 mliap")
+    data = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True, shuffle_pairs_seed=5)
+    ThreePassMLIAP(scaled_model, chunk=80).compute_forces(data)
+    _check("mliap", data.energy, data.eatoms, data.atom_forces(), ref, s.N)
+    _say("case scale/shift/E0 standalone")
+    E, eat, F, PF = ReceiverChunkMACE(scaled_model, chunk=100, device=dev).compute(s)
+    _check("standalone", E, eat, F, ref, s.N)
+    # the bookkeeping is not trivially satisfied: E0 and shift move the energies far beyond the bar
+    e0 = scaled_model.e0.cpu()[s.spidx.long().cpu()] + SHIFT
+    assert float((eat.cpu() - e0).abs().max()) > 1e-3
+
+
+# ----------------------------------------------------------------------------- HIP graphs
+@pytest.mark.parametrize("cache_l1", ["1", "0"])
+def test_mliap_graphs_vs_oracle(dev, scaled_model, scaled_ref, water, cache_l1, monkeypatch):
+    """MACE3P_GRAPHS=1: four full chunks replayed from HIP graphs, over two calls (capture, then replay), against
+    the oracle on the scaled model."""
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    s = water
+    monkeypatch.setenv("MACE3P_GRAPHS", "1")
+    monkeypatch.setenv("MACE3P_CACHE_L1", cache_l1)
+    tp = ThreePassMLIAP(scaled_model, chunk=48)
+    ref = _oracle_sys(scaled_ref, s)
+    for call in range(2):
+        _say(f"case mliap graphs cache_l1={cache_l1} call {call}")
+        data = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True, shuffle_pairs_seed=call or None)
+        tp.compute_forces(data)
+        _check(f"call {call}", data.energy, data.eatoms, data.atom_forces(), ref, s.N)
+    assert tp._rt.gx is not None and tp._rt.gx.n_replays == 24 and tp.n_captures == 1
+
+
+def test_standalone_graphs_vs_oracle(dev, scaled_model, scaled_ref, water):
+    """ReceiverChunkMACE(use_graphs=True): three full chunks of 64 receivers, two calls."""
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
+    s = water
+    ref = _oracle_sys(scaled_ref, s)
+    ev = ReceiverChunkMACE(scaled_model, chunk=64, device=dev, use_graphs=True)
+    for call in range(2):
+        _say(f"case standalone graphs call {call}")
+        E, eat, F, PF = ev.compute(s)
+        _check(f"call {call}", E, eat, F, ref, s.N)
+    assert ev._gx.n_replays == 18
+
+
+# ----------------------------------------------------------------------------- model file
+@pytest.mark.parametrize("recipe", [False, True])
+def test_model_file_vs_oracle(dev, ref_model, water, tmp_path, recipe):
+    """A model file written by make_threepass_model (module or rebuild recipe), unpickled as LAMMPS does, against
+    the oracle of the seed-0 weights."""
+    from mace_onegpu import make_threepass_model
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    s = water
+    path = tmp_path / f"m{int(recipe)}.pt"
+    make_threepass_model.make(str(path), seed=0, chunk=96, recipe=recipe)
+    back = torch.load(str(path), weights_only=False)            # written by this test
+    _say(f"case model file recipe={recipe}")
+    data = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True)
+    back.compute_forces(data)
+    _check("model file", data.energy, data.eatoms, data.atom_forces(), _oracle_sys(ref_model, s), s.N)
+
+
+# ----------------------------------------------------------------------------- MD driver
+@pytest.mark.parametrize("graphs", [False, True])
+def test_md_runner_vs_oracle(dev, scaled_model, scaled_ref, graphs):
+    """MDRunner on 1,536 water atoms (chunks of 700: two full chunks and a tail, or of 512 with graphs): after
+    velocity-Verlet steps and a forced neighbour-list rebuild, the energies and forces of the step equal the
+    oracle's three-pass evaluation on the same positions and the same filtered pairs."""
+    from mace_onegpu import systems
+    from mace_onegpu.md import MDRunner
+    pos, box, Z = systems.water_box(512, seed=1)
+    md = MDRunner(scaled_model, pos, box, Z, chunk=512 if graphs else 700, device=dev, use_graphs=graphs)
+    checks = 0
+    for step in range(4):
+        if step == 2:
+            md._build(md.pos.clone())                 # a rebuild: new Morton order, skin list and chunk templates
+        md.step()
+        if step in (0, 3):
+            _say(f"case md graphs={graphs} step {step} (rebuilds {md.n_rebuild})")
+            pl = md.pairs
+            ref = _oracle(scaled_ref, md.pos.cpu().numpy(), box, (md.Z - 1).cpu().numpy(), pl.NN.cpu().numpy(),
+                          pl.send_view.cpu().numpy(), chunk=384)
+            _check(f"step {step}", md.E, md.eat, md.F, ref, len(pos))
+            checks += 1
+    assert checks == 2 and md.n_rebuild >= 2
+
+
+def test_md_full_size_config5_properties(dev):
+    """Configuration 5 at full size (343,000 molecules, 1,029,000 atoms, chunk 131072): after an MD step and a
+    neighbour-list rebuild, the filtered pair list equals a fresh cell-list build at r_max on the same positions
+    (as sets of atom-id pairs, compared exactly), the forces sum to zero, and the energies are finite."""
+    from mace_onegpu import model as mm, systems
+    from mace_onegpu.md import MDRunner
+    from mace_onegpu.receiver_chunk_mace import System
+    _say("case config5 full size: generating 343,000 molecules")
+    pos, box, Z = systems.water_box(343000, seed=0)
+    N = len(pos)
+    md = MDRunner(mm.MaceModel(seed=0), pos, box, Z, chunk=131072, device=dev)
+    md.step()
+    _say(f"  step 1 done: E {md.E:.6f}")
+    md._build(md.pos.clone())
+    md.forces()
+    _say(f"  after rebuild: E {md.E:.6f}, {md.pairs.E} pairs")
+    pl = md.pairs
+    gid = md.gid
+    recv = torch.repeat_interleave(torch.arange(N, device=dev), pl.NN.long())
+    k_md = torch.sort(gid[recv] * N + gid[pl.send_view.long()]).values
+    fresh = System(md.pos, box, (md.Z - 1).to(torch.int32), 6.0, dev)
+    fresh.build_neighbors()
+    fr = fresh.perm[torch.repeat_interleave(torch.arange(N, device=dev), fresh.NN.long())]
+    fs = fresh.perm[fresh.send.long()]
+    k_fresh = torch.sort(gid[fr] * N + gid[fs]).values
+    _say(f"  fresh build: {k_fresh.numel()} pairs")
+    assert k_md.numel() == k_fresh.numel() and torch.equal(k_md, k_fresh)
+    F = md.F
+    Fsum = float(F.sum(0).abs().max())
+    Fm = float(F.abs().max())
+    _say(f"  sum F {Fsum:.3e} (max|F| {Fm:.3e}), E/N {md.E / N:.8f}")
+    assert np.isfinite(md.E) and bool(torch.isfinite(md.eat).all()) and bool(torch.isfinite(F).all())
+    assert Fsum < 1e-9 * Fm * N and Fm > 0

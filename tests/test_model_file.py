@@ -30,18 +30,18 @@ def test_model_file_roundtrip(tmp_path):
 
 def test_runtime_state_is_not_pickled():
     obj = ThreePassMLIAP(make_threepass_model.MaceModel(seed=1))
-    obj._fl, obj._gx, obj._l1cache, obj._loc = object(), object(), object(), object()
+    obj._rt, obj.last_timings = object(), {"A": 1.0}
     d = obj.__getstate__()
-    assert not {"_fl", "_gx", "_l1cache", "_loc"} & set(d)
+    assert not {"_rt", "last_timings"} & set(d)
     back = pickle.loads(pickle.dumps(obj))
-    assert not hasattr(back, "_fl") and _same_weights(back.model, obj.model)
+    assert back._rt is None and back.last_timings is None and _same_weights(back.model, obj.model)
 
 
 def test_rebuild_recipe(tmp_path):
     out = tmp_path / "m3pr.pt"
     obj = make_threepass_model.make(str(out), seed=3, recipe=True)
     back = torch.load(str(out), weights_only=False)
-    assert "model" not in back.__dict__ and back._rebuild is not None
+    assert "model" not in back.__dict__ and back._recipe is not None
     assert _same_weights(back._rebuild_model(), obj.model)
 
 
