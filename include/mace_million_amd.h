@@ -2,8 +2,8 @@
  * energy + force evaluation.
  *
  * Conventions (all entry points):
- *   - return 0 on success, a negative code on failure (-1 invalid argument, -2 launch failure); the message of the
- *     last failure of the calling thread is mm_last_error();
+ *   - return 0 on success, a negative code on failure (-1 invalid argument, -2 launch failure, -3 size beyond a
+ *     fixed limit); the message of the last failure of the calling thread is mm_last_error();
  *   - pointers are device pointers unless marked HOST; sizes are element counts; `stream` is a hipStream_t;
  *   - no entry point allocates, frees or synchronises: the caller owns every buffer, and every call can be
  *     captured into a HIP graph;
@@ -46,6 +46,11 @@ int mm_nl_count(const double* pos_sorted, const int* cell_sorted, long N, const 
                 const int* ncell /* HOST [3] */, const int* cell_start, const int* cell_count, double r_cut2,
                 int brute, int* NN, mm_stream_t stream);
 int mm_nl_scan(const int* NN, long* rowptr, long N, void* workspace, size_t workspace_bytes, mm_stream_t stream);
+/* No counterpart in the reference.  mm_nl_scan without a workspace, for callers that cannot allocate one (code
+ * under HIP-graph capture, tight serving loops): the tile partials live in a static device array of the library
+ * (256 KiB per GPU, held until the process ends).  Limit: N + 1 <= 134,217,728, larger N returns MM_ERANGE.
+ * Calls that overlap on one GPU share the array and race. */
+int mm_nl_scan_noalloc(const int* NN, long* rowptr, long N, mm_stream_t stream);
 int mm_nl_fill(const double* pos_sorted, const int* cell_sorted, long N, const double* box /* HOST [3] */,
                const int* ncell /* HOST [3] */, const int* cell_start, const int* cell_count, double r_cut2,
                int brute, const long* rowptr, int* send, mm_stream_t stream);

@@ -14,6 +14,9 @@
 
 #include <hipcub/hipcub.hpp>
 
+#include <mutex>
+#include <string>
+
 __global__ void mm_nl_prepare_kernel(const double* __restrict__ pos_in, long N, double bx, double by, double bz,
                                      double cx, double cy, double cz, int nx, int ny, int nz,
                                      double* __restrict__ pos_w, int* __restrict__ cell,
@@ -211,6 +214,137 @@ extern "C" int mm_nl_scan(const int* NN, long* rowptr, long N, void* ws, size_t 
   MM_CHECK_ARG(ws_bytes >= need, "workspace too small");
   hipcub::DeviceScan::ExclusiveSum(ws, need, it, rowptr, (int)N + 1, stream);
   return mm::launch_status("mm_nl_scan");
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Allocation-free receiver-CSR scan (no counterpart in the reference).  mm_nl_scan_noalloc gives the result of
+// mm_nl_scan (rowptr[0] = 0, rowptr[i + 1] = sum_{j <= i} NN[j], int64) without a workspace argument, for callers
+// that cannot allocate one (code under HIP-graph capture, serving loops).  Its tile partials live in `scratch`, a
+// file-scope device array that every GPU the library runs on holds until the process ends:
+//   * N + 1 <= MM_SCAN_MAX_TILES * MM_SCAN_TILE = 134,217,728 counts (larger N is rejected with MM_ERANGE);
+//   * the array's device address is looked up once per device (hipGetSymbolAddress, first call on that device);
+//   * every partial is written before it is read within one call, so nothing needs clearing between calls;
+//   * calls that overlap on one GPU (different streams) share the array and race.
+// Three kernels: per-tile sums -> one block scans the tile sums in place -> per-tile scan plus its offset.
+#define MM_SCAN_THREADS 256
+#define MM_SCAN_ITEMS 16
+#define MM_SCAN_TILE (MM_SCAN_THREADS * MM_SCAN_ITEMS)
+#define MM_SCAN_MAX_TILES 32768
+#define MM_SCAN_OFFSET_THREADS 1024
+
+static __device__ __align__(256) long long scratch[MM_SCAN_MAX_TILES];
+
+// item i of the scan: NN[i] for i < N, 0 for i = N (the appended zero that makes rowptr[N] the total)
+__device__ __forceinline__ long long mm_scan_item(const int* __restrict__ NN, long N, long i) {
+  return i < N ? (long long)NN[i] : 0LL;
+}
+
+// In-place inclusive scan of v[0..n) (n = blockDim.x threads, one value each) in LDS; returns the inclusive value
+// of this thread.
+__device__ __forceinline__ long long mm_block_inclusive_scan(long long x, long long* lds) {
+  const int t = threadIdx.x;
+  lds[t] = x;
+  __syncthreads();
+  for (int d = 1; d < (int)blockDim.x; d <<= 1) {
+    const long long y = t >= d ? lds[t - d] : 0LL;
+    __syncthreads();
+    lds[t] += y;
+    __syncthreads();
+  }
+  return lds[t];
+}
+
+__global__ void __launch_bounds__(MM_SCAN_THREADS) mm_scan_tile_sums_kernel(const int* __restrict__ NN, long N,
+                                                                             long long* __restrict__ part) {
+  __shared__ long long lds[MM_SCAN_THREADS];
+  const long base = (long)blockIdx.x * MM_SCAN_TILE + (long)threadIdx.x * MM_SCAN_ITEMS;
+  long long s = 0;
+#pragma unroll
+  for (int k = 0; k < MM_SCAN_ITEMS; ++k) s += mm_scan_item(NN, N, base + k);
+  const long long tot = mm_block_inclusive_scan(s, lds);
+  if (threadIdx.x == MM_SCAN_THREADS - 1) part[blockIdx.x] = tot;
+}
+
+// One block: part[0..tiles) <- exclusive prefix sums of the tile sums.
+__global__ void __launch_bounds__(MM_SCAN_OFFSET_THREADS) mm_scan_tile_offsets_kernel(long long* __restrict__ part,
+                                                                                        int tiles) {
+  __shared__ long long lds[MM_SCAN_OFFSET_THREADS];
+  const int per = (tiles + MM_SCAN_OFFSET_THREADS - 1) / MM_SCAN_OFFSET_THREADS;
+  const int lo = threadIdx.x * per;
+  const int hi = min(lo + per, tiles);
+  long long s = 0;
+  for (int i = lo; i < hi; ++i) s += part[i];
+  long long run = mm_block_inclusive_scan(s, lds) - s;     // exclusive prefix of this thread's run
+  for (int i = lo; i < hi; ++i) {
+    const long long v = part[i];
+    part[i] = run;
+    run += v;
+  }
+}
+
+__global__ void __launch_bounds__(MM_SCAN_THREADS) mm_scan_tile_apply_kernel(const int* __restrict__ NN, long N,
+                                                                              const long long* __restrict__ part,
+                                                                              long* __restrict__ rowptr) {
+  __shared__ long long lds[MM_SCAN_THREADS];
+  const long base = (long)blockIdx.x * MM_SCAN_TILE + (long)threadIdx.x * MM_SCAN_ITEMS;
+  long long v[MM_SCAN_ITEMS];
+  long long s = 0;
+#pragma unroll
+  for (int k = 0; k < MM_SCAN_ITEMS; ++k) {
+    v[k] = mm_scan_item(NN, N, base + k);
+    s += v[k];
+  }
+  long long run = mm_block_inclusive_scan(s, lds) - s + part[blockIdx.x];
+#pragma unroll
+  for (int k = 0; k < MM_SCAN_ITEMS; ++k) {
+    if (base + k <= N) rowptr[base + k] = (long)run;
+    run += v[k];
+  }
+}
+
+namespace {
+std::mutex g_scratch_mu;
+long long* g_scratch_ptr[64] = {};     // device address of `scratch` per device ordinal
+
+int scan_scratch(long long** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    mm::set_error("mm_nl_scan_noalloc: no current HIP device");
+    return MM_ELAUNCH;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      mm::set_error(std::string("mm_nl_scan_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      return MM_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = (long long*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MM_OK;
+}
+}  // namespace
+
+extern "C" int mm_nl_scan_noalloc(const int* NN, long* rowptr, long N, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && rowptr && (N == 0 || NN), "bad arguments");
+  const long tiles = (N + 1 + MM_SCAN_TILE - 1) / MM_SCAN_TILE;
+  if (tiles > MM_SCAN_MAX_TILES) {
+    mm::set_error("mm_nl_scan_noalloc: N = " + std::to_string(N) + " exceeds the scratch limit N + 1 <= " +
+                  std::to_string((long)MM_SCAN_MAX_TILES * MM_SCAN_TILE) + " (use mm_nl_scan with a workspace)");
+    return MM_ERANGE;
+  }
+  long long* part = nullptr;
+  const int rc = scan_scratch(&part);
+  if (rc != MM_OK) return rc;
+  hipLaunchKernelGGL(mm_scan_tile_sums_kernel, dim3((unsigned)tiles), dim3(MM_SCAN_THREADS), 0, stream, NN, N,
+                     part);
+  hipLaunchKernelGGL(mm_scan_tile_offsets_kernel, dim3(1), dim3(MM_SCAN_OFFSET_THREADS), 0, stream, part,
+                     (int)tiles);
+  hipLaunchKernelGGL(mm_scan_tile_apply_kernel, dim3((unsigned)tiles), dim3(MM_SCAN_THREADS), 0, stream, NN, N,
+                     (const long long*)part, rowptr);
+  return mm::launch_status("mm_nl_scan_noalloc");
 }
 
 extern "C" int mm_nl_fill(const double* pos_s, const int* cell_s, long N, const double* box, const int* ncell,

@@ -33,6 +33,7 @@ SIGNATURES = {
     "mm_nl_cell_ranges": [P, L, P, P, P, P],
     "mm_nl_count": [P, P, L, P, P, P, P, D, I, P, P],
     "mm_nl_scan": [P, P, L, P, SZ, P],
+    "mm_nl_scan_noalloc": [P, P, L, P],
     "mm_nl_fill": [P, P, L, P, P, P, P, D, I, P, P, P],
     "mm_nl_filter_count": [P, L, P, P, P, D, P, P],
     "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P, P],
