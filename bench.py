@@ -15,16 +15,22 @@ the initial force call, then K timed steps between synchronisations.
                vectors (unit directions x U[0.8, 6.0] A), features and cotangents; value = achieved algorithmic GB/s of
                the layer-2 forward kernel, every kernel listed
 Objects beside the contract fields:
-  roofline     : the dominant kernel, algorithmic bytes per launch / mean launch time measured with HIP events on the
-                 launch stream during the timed steps, against 8 TB/s HBM; traffic = measured HBM bytes per launch
-                 from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload (or null)
+  roofline     : the dominant kernel, algorithmic bytes (or FLOPs) per launch / mean launch time measured with HIP
+                 events on the launch stream during the timed steps.  bound: "valu" for the edge convolutions (fp32
+                 v_fma_f32 on the vector ALUs; peak 78.6 TFLOP/s, packed-FP32 instructions being disabled in this
+                 build -- frac_of_fp32_chip_peak is the fraction of the 157.3 TFLOP/s chip figure), "mfma" for the
+                 matrix-core kernels, "hbm" below the ridge; traffic = measured HBM bytes per launch from the
+                 committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload (or null)
   node_kernels : the linears (bf16 MFMA: mfma_frac = 6 F / t / 2.5 PFLOP/s; fp32_equiv_frac = F / t / 157.3) and the
-                 symmetric contractions (HBM roof) timed with HIP events in one extra step after the timed ones, with
-                 algorithmic bytes and FLOPs
-  step_roofline: atom-steps/s against the fp32 MFMA ceiling of the exact model's work per atom-step (edge terms,
-                 node linears and the symmetric contractions S1 / S2 per node)
-  cpu_baseline : the fp64 CPU oracle (oracle/mace_ref.py, a restatement of the reference's three-pass algorithm) on a
-                 bounded sample of the same workload, in the metric's unit
+                 symmetric contractions (HBM roof; FLOPs = the operations the generated kernels execute) timed with
+                 HIP events in one extra step after the timed ones
+  step_roofline: atom-steps/s against the fp32 ceiling of the exact model's work per atom-step (edge terms, node
+                 linears, and the symmetric contractions at the operations the kernels execute)
+  cpu_baseline : the fp32 torch-CPU restatement of the production three-pass algorithm (oracle/cpu_fp32.py: spline
+                 tables, passes A / B / C) timed on one 16,384-receiver chunk of the same system and extrapolated to
+                 all chunks, in the metric's unit
+  configs      : (default run) configurations 3, 4 and 2 measured in the same process after configuration 5, each
+                 with its value, dominant-kernel roofline and per-kernel table
 """
 import argparse
 import json
@@ -37,6 +43,7 @@ sys.path.insert(0, os.path.join(ROOT, "mace-million_amd"))
 
 HBM_PEAK_GBS = 8000.0
 VALU_F32_PEAK_TFLOPS = 78.6      # fp32 vector FMA without packed-FP32 instructions (the build disables them)
+FP32_CHIP_PEAK_TFLOPS = 157.3    # MI355X fp32 figure (vector with packed FP32, or MFMA)
 MFMA_F32_PEAK_TFLOPS = 157.3
 MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA (the linears: fp32 products as six bf16 products)
 C = 128
@@ -120,9 +127,9 @@ def node_algorithmic(name, units, symc_flops):
     linear (mm_linear, MFMA): units (rows, sum of K-chunks, distinct input blocks, output components, accumulate,
       distinct 128 x 128 weight blocks): 2 * 128 * 128 flops per row and K-chunk; each input block and output
       component read / written once per row (accumulating outputs read too), each weight block once.
-    symc<L>_<dir>: units (rows,): symc_flops[(L, dir)] flops per row (the dense-coefficient count of the model's
-      contraction, backward = 2 x forward); bytes: the 16-component input, the output (layer 1: 4 components,
-      layer 2: 1), the backward's cotangent in and gradient out, the species index and density terms."""
+    symc<L>_<dir>: units (rows,): symc_flops[(L, dir)] flops per row (the operations the generated kernel executes);
+      bytes: the 16-component input, the output (layer 1: 4 components, layer 2: 1), the backward's cotangent in
+      and gradient out, the species index and density terms."""
     if name == "linear":
         rows, k_sum, n_in, n_comp, acc, n_w = units
         return 4 * C * rows * (n_in + n_comp * (1 + acc)) + 4 * C * C * n_w, 2 * C * C * rows * k_sum
@@ -135,12 +142,24 @@ def node_algorithmic(name, units, symc_flops):
     return 4 * C * rows * (16 + n_out + 16) + 12 * rows, F
 
 
-def symc_flops_per_row(tables):
-    """{(layer, 'fwd' | 'bwd'): flops per node} of the two symmetric contractions (S1, S2 forward; 2x backward)."""
+def symc_flops_per_row(tables=None):
+    """{(layer, 'fwd' | 'bwd'): floating-point operations per node} that the generated symmetric-contraction kernels
+    execute, counted from their gfx950 assembly by the build (lib/kernel_ops.json)."""
     from mace_onegpu import codegen
-    S1 = codegen.symc_model_flops(tables.sc1, [0, 1])
-    S2 = codegen.symc_model_flops(tables.sc2, [0])
-    return {(1, "fwd"): S1, (1, "bwd"): 2 * S1, (2, "fwd"): S2, (2, "bwd"): 2 * S2}
+    gen = os.path.join(ROOT, "mace-million_amd", "csrc", "gen")
+    ops = os.path.join(ROOT, "mace-million_amd", "lib", "kernel_ops.json")
+    out = {}
+    for layer in (1, 2):
+        for d, f in codegen.symc_executed_flops(gen, layer, ops_json=ops).items():
+            out[(layer, d)] = f
+    return out
+
+
+def symc_dense_flops(tables):
+    """S1, S2 by the reference's dense-coefficient convention (scripts/flop_budget.py:53-56): 2 (nu + 1) flops per
+    non-zero of each path's coupling tensor and channel."""
+    from mace_onegpu import codegen
+    return codegen.symc_model_flops(tables.sc1, [0, 1]), codegen.symc_model_flops(tables.sc2, [0])
 
 
 def node_kernel_table(fl, ktimes, steps):
@@ -161,14 +180,26 @@ def summarize(name, launches, ms_total, B, F, steps):
     k = dict(launches=launches, ms_per_launch=ms_total / launches, ms_per_step=ms_total / steps,
              GBps=B / sec / 1e9, TFLOPs=F / sec / 1e12, hbm_frac=B / sec / 1e9 / HBM_PEAK_GBS,
              bytes_per_launch=B / launches, flops_per_launch=F / launches)
+    eng = engine(name)
+    k["engine"] = eng
     if name.startswith("ace1"):          # fp32 MFMA
         k["mfma_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
     elif name == "linear":               # six bf16 MFMA products per fp32 product
         k["mfma_frac"] = 6 * F / sec / 1e12 / MFMA_BF16_PEAK_TFLOPS
         k["fp32_equiv_frac"] = F / sec / 1e12 / MFMA_F32_PEAK_TFLOPS
-    elif not name.startswith("symc"):    # the contractions' count is a convention above the executed work: HBM roof
+    else:                                # vector ALUs (executed operations)
         k["valu_frac"] = F / sec / 1e12 / VALU_F32_PEAK_TFLOPS
     return k
+
+
+def engine(name):
+    """The unit a kernel's arithmetic runs on: the edge convolutions and the symmetric contractions are fp32 VALU
+    code (v_fma_f32), the layer-1 ACE kernels fp32 MFMA, the linears bf16 MFMA."""
+    if name.startswith("ace1"):
+        return "mfma_f32"
+    if name == "linear":
+        return "mfma_bf16"
+    return "valu"
 
 
 def kernel_table(fl, ktimes, steps):
@@ -184,19 +215,23 @@ def kernel_table(fl, ktimes, steps):
 
 
 def roofline_of(kernels, workload=None):
-    """Roofline of the dominant kernel: fraction = max(B / 8 TB/s, F / 157.3 TFLOP/s) / t -- the HBM roof for
-    kernels below the ridge (19.7 flop/B), the fp32 compute roof above it (the edge convolutions: 100-300 flop/B).
-    Both the HBM figures and the compute figures are reported."""
+    """Roofline of the dominant kernel (most time per step): the compute roof of the unit it runs on (VALU 78.6,
+    fp32 MFMA 157.3 TFLOP/s) when its intensity is above that unit's ridge with 8 TB/s, the HBM roof below it.
+    Both the HBM and the compute figures are reported."""
     if not kernels:
         return None
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])
     k = kernels[dom]
     intensity = k["flops_per_launch"] / k["bytes_per_launch"]
-    compute = intensity > MFMA_F32_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)
+    eng = k.get("engine", engine(dom))
+    peak = {"valu": VALU_F32_PEAK_TFLOPS, "mfma_f32": MFMA_F32_PEAK_TFLOPS,
+            "mfma_bf16": MFMA_F32_PEAK_TFLOPS}[eng]
+    compute = intensity > peak * 1e12 / (HBM_PEAK_GBS * 1e9)
     out = {"kernel": f"mm_{dom}_kernel"}
     if compute:
-        out.update({"bound": "mfma", "achieved": round(k["TFLOPs"], 3), "peak": MFMA_F32_PEAK_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(k["TFLOPs"] / MFMA_F32_PEAK_TFLOPS, 4)})
+        out.update({"bound": "valu" if eng == "valu" else "mfma", "achieved": round(k["TFLOPs"], 3), "peak": peak,
+                    "unit": "TFLOP/s", "frac": round(k["TFLOPs"] / peak, 4),
+                    "frac_of_fp32_chip_peak": round(k["TFLOPs"] / FP32_CHIP_PEAK_TFLOPS, 4)})
     else:
         out.update({"bound": "hbm", "achieved": round(k["GBps"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(k["hbm_frac"], 5)})
@@ -207,115 +242,112 @@ def roofline_of(kernels, workload=None):
                 **{f: round(k[f], 4) for f in ("valu_frac", "mfma_frac") if f in k},
                 "bytes_per_launch": int(k["bytes_per_launch"]), "flops_per_launch": int(k["flops_per_launch"]),
                 "ms_per_launch": round(k["ms_per_launch"], 4), "launches": k["launches"]})
-    if compute and "valu_frac" in k:
-        out["note"] = ("fp32 compute roof: the kernel runs on the vector ALUs (v_fma_f32); with packed-FP32 "
-                       "instructions disabled their peak is 78.6 TFLOP/s (valu_frac)")
+    if compute and eng == "valu":
+        out["note"] = ("the kernel runs on the vector ALUs (v_fma_f32); peak 78.6 TFLOP/s = 256 CUs x 64 lanes x "
+                       "2 flops x 2.4 GHz without packed-FP32 instructions, which this build disables; "
+                       "frac_of_fp32_chip_peak is against the 157.3 TFLOP/s chip figure")
     return out
 
 
 def step_roofline(value, pairs_per_atom, tables):
     """Work of the exact model per atom-step (the reference's three-pass algorithm: layer-1 conv forward in pass A
     and forward + backward in pass C, layer-2 conv forward + backward in pass B, at 2 flops per FMA; node-level
-    linears 4 L1node + 3 L2node) and the fp32 MFMA ceiling it implies."""
+    linears 4 L1node + 3 L2node; the symmetric contractions at the operations the generated kernels execute,
+    forward + backward of layer 1 twice and of layer 2 once) and the fp32 ceiling it implies."""
     t1, t2 = tables.tp1, tables.tp2
     n1, w1, n2, w2 = len(t1["terms"]), t1["nW"], len(t2["terms"]), t2["nW"]
     edge = pairs_per_atom * 2 * C * ((n1 + 4 * w1) * 2 + (2 * n1 + 8 * w1) + (n2 + 4 * w2) + (3 * n2 + 8 * w2))
     l1node = 2 * C * C * (16 + 16 + 4)
     l2node = 2 * C * C * (40 + 4 * 1.83 + 1 + 1)
-    sf = symc_flops_per_row(tables)
-    S1, S2 = sf[(1, "fwd")], sf[(2, "fwd")]
-    f_atom = edge + 4 * l1node + 3 * l2node + 4 * S1 + 3 * S2
-    ceiling = MFMA_F32_PEAK_TFLOPS * 1e12 / f_atom
-    return {"flop_per_atom_step": round(f_atom), "ceiling_atom_steps_per_s": round(ceiling), "peak_TFLOPs":
-            MFMA_F32_PEAK_TFLOPS, "frac": round(value / ceiling, 4), "S1_flop_per_node": S1, "S2_flop_per_node": S2,
-            "note": "S1, S2: forward symmetric-contraction FLOPs per node, 2 (nu + 1) per non-zero of each path's "
-                    "coupling tensor and channel (backward 2x forward); the evaluated algorithm does less work (layer "
-                    "1 in the density-projection form, pass C reuses pass A's layer-1 state, factorised contractions)"}
+    sf = symc_flops_per_row()
+    symc = 2 * sf[(1, "fwd")] + sf[(1, "bwd")] + sf[(2, "fwd")] + sf[(2, "bwd")]
+    f_atom = edge + 4 * l1node + 3 * l2node + symc
+    ceiling = FP32_CHIP_PEAK_TFLOPS * 1e12 / f_atom
+    S1d, S2d = symc_dense_flops(tables)
+    return {"flop_per_atom_step": round(f_atom), "ceiling_atom_steps_per_s": round(ceiling),
+            "peak_TFLOPs": FP32_CHIP_PEAK_TFLOPS, "frac": round(value / ceiling, 4),
+            "symc_flop_per_node_step": symc, "S1_dense_flop_per_node": S1d, "S2_dense_flop_per_node": S2d,
+            "note": "edge and linear terms count the reference algorithm's work (this build executes less: layer 1 "
+                    "in the density-projection form, pass C reuses pass A's layer-1 state); the symmetric "
+                    "contractions count the operations the generated kernels execute, not the dense-coefficient "
+                    "convention (S1/S2_dense, shown for comparison)"}
 
 
 def ncores():
-    return len(os.sched_getaffinity(0))
+    """Host threads this run may use: the affinity mask, capped by OMP_NUM_THREADS when it is set (the box's
+    CPU share for one GPU)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else n
 
 
-def cpu_baseline_water(n_mol=1024, seed=0):
-    """fp64 CPU oracle, one full E+F of a water box from the same generator."""
+def cpu_baseline_chunk(pos, box, spec, NN, send, chunk=16384, label=""):
+    """fp32 torch-CPU restatement of the production three-pass algorithm (oracle/cpu_fp32.py: the oracle's layer
+    functions in fp32 with the 512-knot Hermite tables) timed on the first `chunk` receivers of this system -- one
+    receiver chunk of each pass -- and extrapolated to every chunk of the system, in atom-steps/s.  Inputs are
+    the system's own positions, species and pair list (host copies)."""
     import numpy as np
     import torch
 
     sys.path.insert(0, ROOT)
-    from mace_onegpu import model as mm, o3, systems
-    from oracle import mace_ref, neighbors
+    from mace_onegpu import model as mm, o3
+    from oracle import cpu_fp32, mace_ref
 
     torch.set_num_threads(ncores())
-    model = mm.MaceModel(seed=0)
-    m = mace_ref.RefModel(model, o3.coupling)
-    pos, box, Z = systems.water_box(n_mol, seed=seed)
-    s = neighbors.SystemRef(pos, box, Z - 1, 6.0)
-    NN, rp, send = s.build_neighbors()
-    recv = np.repeat(np.arange(s.N), NN)
-    mace_ref.silu_norm()
-    t0 = time.perf_counter()
-    mace_ref.three_pass(m, s.pos, box, s.spidx, recv, send, chunk=512)
-    dt = time.perf_counter() - t0
-    return dict(value=s.N / dt, unit="atom-steps/s", cores=ncores(), kind="port",
-                sample=f"fp64 CPU oracle (oracle/mace_ref.three_pass), one E+F of a {n_mol}-molecule water box "
-                       f"({s.N} atoms, {len(send)} pairs, chunk 512), {dt:.1f} s on {ncores()} threads")
+    m = mace_ref.RefModel(mm.MaceModel(seed=0), o3.coupling)
+    N = len(pos)
+    t32 = mace_ref.Tables64(m, sorted(set(np.asarray(spec).tolist())), n_grid=512).astype(torch.float32)
+    rowptr = np.concatenate([[0], np.cumsum(NN)])
+    b = min(chunk, N)
+    r = cpu_fp32.chunk_timing(m.astype(torch.float32), t32, pos, box, spec, rowptr, send, 0, b, sub=512)
+    t_chunk = r["topology"] + r["A"] + r["B"] + r["C"]
+    n_chunks = N / b
+    value = N / (t_chunk * n_chunks)
+    return dict(value=round(value, 2), unit="atom-steps/s", cores=ncores(), kind="port",
+                sample=f"fp32 torch-CPU restatement of the three-pass algorithm with 512-knot spline tables "
+                       f"(oracle/cpu_fp32.py) on receivers [0, {b}) of {label} ({r['edges']} edges): topology "
+                       f"{r['topology']:.1f} s, pass A {r['A']:.1f} s, B {r['B']:.1f} s, C {r['C']:.1f} s = "
+                       f"{t_chunk:.1f} s per chunk on {ncores()} threads, extrapolated to {n_chunks:.2f} chunks "
+                       f"of {b} receivers ({N} atoms)",
+                extrapolated=True, seconds_per_chunk=round(t_chunk, 2))
 
 
-def cpu_baseline_fcc(n_cells=5):
-    import numpy as np
+def cpu_baseline_conv(rij, recv_local, ls, rowptr, E_full, nC_full, nN_full, n_recv=512):
+    """fp32 torch-CPU layer-2 edge convolution of the restatement (512-knot table lookup of W, channelwise TP over
+    the sparse path table, receiver sum) on the first n_recv receivers of the config-2 chunk, scaled to the chunk's
+    edges and expressed in the metric's unit (algorithmic GB/s of mm_conv2_fwd over the whole chunk)."""
     import torch
 
     sys.path.insert(0, ROOT)
-    from mace_onegpu import model as mm, o3, systems
-    from oracle import mace_ref, neighbors
-
-    torch.set_num_threads(ncores())
-    model = mm.MaceModel(seed=0)
-    m = mace_ref.RefModel(model, o3.coupling)
-    pos, box, Z = systems.fcc_alloy(n_cells=n_cells)
-    s = neighbors.SystemRef(pos, box, Z - 1, 6.0)
-    NN, rp, send = s.build_neighbors()
-    recv = np.repeat(np.arange(s.N), NN)
-    mace_ref.silu_norm()
-    t0 = time.perf_counter()
-    mace_ref.three_pass(m, s.pos, box, s.spidx, recv, send, chunk=512)
-    dt = time.perf_counter() - t0
-    return dict(value=s.N / dt, unit="atom-steps/s", cores=ncores(), kind="port",
-                sample=f"fp64 CPU oracle (oracle/mace_ref.three_pass), one E+F of a {n_cells}^3-cell FCC Fe/Ni/Cr/Co "
-                       f"box ({s.N} atoms, {len(send)} pairs), {dt:.1f} s on {ncores()} threads")
-
-
-def cpu_baseline_conv(E_full, nC_full, nN_full, E_sample=40000):
-    """fp32 torch-CPU channelwise TP (oracle.mace_ref.channelwise_tp + scatter_sum) of layer 2 on a sample of edges,
-    scaled to the config-2 chunk and expressed in its unit (algorithmic GB/s of the layer-2 forward over the chunk's
-    E_full edges)."""
-    import torch
-
-    sys.path.insert(0, ROOT)
-    from mace_onegpu import o3
+    from mace_onegpu import model as mm, o3
     from mace_onegpu.fused_conv import ChannelwiseTP
     from oracle import mace_ref
 
     torch.set_num_threads(ncores())
+    m = mace_ref.RefModel(mm.MaceModel(seed=0), o3.coupling)
+    t32 = mace_ref.Tables64(m, [0, 7], n_grid=512).astype(torch.float32)
     d = ChannelwiseTP([0, 1])
-    g = torch.Generator().manual_seed(0)
-    n = E_sample // 90
-    X = torch.randn(n, d.nX, C, generator=g)
-    Y = torch.randn(E_sample, 16, generator=g)
-    W = torch.randn(E_sample, d.nW, C, generator=g)
-    send = torch.randint(0, n, (E_sample,), generator=g)
-    recv = torch.sort(torch.randint(0, n, (E_sample,), generator=g)).values
+    ne = int(rowptr[n_recv])
+    vec = torch.as_tensor(rij[:ne]).float()
+    lr = torch.as_tensor(recv_local[:ne]).long()
+    send = torch.as_tensor(ls[:ne]).long()
+    n = int(send.max()) + 1
+    X = torch.randn(n, d.nX, C, generator=torch.Generator().manual_seed(2))
+    pair = torch.zeros(ne, dtype=torch.long)
     t0 = time.perf_counter()
+    r = torch.linalg.vector_norm(vec, dim=1)
+    W = t32.lookup(1, r, pair).reshape(ne, d.nW, C)
+    Y = mace_ref.sh(vec)
     mid = mace_ref.channelwise_tp(W, X, Y, send, d.table["paths"], d.table["in_ls"], o3.coupling)
-    mace_ref.scatter_sum(mid, recv, n)
+    mace_ref.scatter_sum(mid, lr, n_recv)
     dt = time.perf_counter() - t0
     B, _ = conv_algorithmic("conv2_fwd", E_full, nC_full, nN_full, d.table)
-    t_full = dt * E_full / E_sample
-    return dict(value=B / t_full / 1e9, unit="GB/s", cores=ncores(), kind="port",
-                sample=f"torch-CPU fp32 channelwise TP + receiver sum of layer 2 (oracle/mace_ref.channelwise_tp, "
-                       f"explicit weights) on {E_sample} edges, {dt:.2f} s on {ncores()} threads, scaled to the "
-                       f"chunk's {E_full} edges ({t_full:.1f} s); bytes counted as for mm_conv2_fwd")
+    t_full = dt * E_full / ne
+    return dict(value=round(B / t_full / 1e9, 3), unit="GB/s", cores=ncores(), kind="port",
+                sample=f"fp32 torch-CPU layer-2 convolution of the restatement (table lookup of W, channelwise TP, "
+                       f"receiver sum; oracle/mace_ref.py) on the chunk's first {n_recv} receivers ({ne} edges), "
+                       f"{dt:.2f} s on {ncores()} threads, scaled to the chunk's {E_full} edges ({t_full:.1f} s); "
+                       f"bytes counted as for mm_conv2_fwd", extrapolated=True)
 
 
 def exit_multi_gpu():
@@ -387,7 +419,11 @@ def run_md(a):
     value = N * a.steps / dt
     kernels = kernel_table(fl, ktimes, a.steps)
     roof = roofline_of(kernels, {"n_mol": a.n_mol, "chunk": a.chunk})
-    cpu = None if a.no_cpu else cpu_baseline_water()
+    cpu = None
+    if not a.no_cpu:
+        print("# cpu baseline: one 16,384-receiver chunk of this system", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_chunk(md.pos.cpu().numpy(), box, (md.Z - 1).cpu().numpy(), md.pairs.NN.cpu().numpy(),
+                                 md.pairs.send_view.cpu().numpy(), 16384, "the configuration-5 water box")
     line = base_line(a, "atom-steps/s (E+F, 1M-atom water, fp32, 1 GPU)", value, dt / a.steps * 1e3, "atom-steps/s",
                      "synthetic (seeded water generator, random-init weights)",
                      {"workload": "config5: 343,000-molecule water (1,029,000 atoms), random-init MPA-0-medium "
@@ -440,15 +476,29 @@ def run_ef(a):
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
     value = s.N * a.steps / dt
-    kernels = kernel_table(fl, ktimes, a.steps) if not graphs else {}
-    nodes = {}
-    if not graphs:      # one more evaluation with the linears' and contractions' launches timed as well
-        fl.start_kernel_timing(node_kernels=True)
-        ev.compute(s)
-        nodes = node_kernel_table(fl, fl.stop_kernel_timing(), 1)
+    if graphs:
+        # HIP events cannot time launches inside graph replays: one eager evaluation of the same system, with every
+        # launch timed, gives the per-kernel table (the same kernels the graphs replay)
+        eager = ReceiverChunkMACE(model, chunk=chunk, device="cuda", use_graphs=False)
+        eager.compute(s)
+        fl = eager.fl
+        fl.start_kernel_timing()
+        eager.compute(s)
+        kernels = kernel_table(fl, fl.stop_kernel_timing(), 1)
+        ev_nodes = eager
+    else:
+        kernels = kernel_table(fl, ktimes, a.steps)
+        ev_nodes = ev
+    fl.start_kernel_timing(node_kernels=True)   # one more evaluation with the node-level launches timed as well
+    ev_nodes.compute(s)
+    nodes = node_kernel_table(fl, fl.stop_kernel_timing(), 1)
     cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline_water() if a.config == 3 else cpu_baseline_fcc()
+    if a.cpu_from is not None:
+        cpu = dict(a.cpu_from)
+    elif not a.no_cpu:
+        print(f"# cpu baseline: one 16,384-receiver chunk of configuration {a.config}", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_chunk(s.pos.cpu().numpy(), s.box, s.spidx.cpu().numpy(), s.NN.cpu().numpy(),
+                                 s.send.cpu().numpy(), 16384, f"the configuration-{a.config} system")
     n_pairs = int(s.rowptr[-1])
     line = base_line(a, metric, value, dt / a.steps * 1e3, "atom-steps/s",
                      "synthetic (seeded generator, random-init weights)",
@@ -457,9 +507,9 @@ def run_ef(a):
                       "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2)},
                      roofline_of(kernels), kernels, cpu)
     if graphs:
-        line["roofline_note"] = "per-kernel HIP-event timing is not available inside graph replays (rocprofv3)"
-    else:
-        line["node_kernels"] = rounded(nodes)
+        line["roofline_note"] = ("kernels timed with HIP events in one eager evaluation of the same system after the "
+                                 "graph-replayed steps (events cannot time launches inside a replay)")
+    line["node_kernels"] = rounded(nodes)
     line["step_roofline"] = step_roofline(value, n_pairs / s.N, fl.tables)
     return line
 
@@ -575,7 +625,10 @@ def run_conv(a):
     ref = tp(X2, Yc, Wsp, ei)[:nr]
     err = float((ref - out2[:nr]).abs().max() / ref.abs().max())
     v = kernels["conv2_fwd"]
-    cpu = None if a.no_cpu else cpu_baseline_conv(E, nC, nN)
+    cpu = None
+    if not a.no_cpu:
+        rp_h = g.rowptr.cpu().numpy()
+        cpu = cpu_baseline_conv(g.rij.cpu().numpy(), g.recv_local.cpu().numpy(), g.ls.cpu().numpy(), rp_h, E, nC, nN)
     line = base_line(a, "edge-conv achieved algorithmic GB/s (layer-2 forward, one 16,384-receiver chunk)", v["GBps"],
                      v["ms_per_launch"], "GB/s",
                      "synthetic (config-3 topology; random unit directions x U[0.8, 6] A, N(0,1) features and "
@@ -587,12 +640,29 @@ def run_conv(a):
     return line
 
 
+def sub_line(line):
+    """The summary of a configuration measured inside the default run."""
+    keep = ("metric", "value", "unit", "steps", "warmup", "ms_per_step", "higher_is_better", "config", "roofline",
+            "kernels", "node_kernels", "step_roofline", "cpu_baseline", "roofline_note", "steps_note")
+    return {k: line[k] for k in keep if k in line}
+
+
+def free_gpu():
+    import gc
+
+    import torch
+    gc.collect()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=5, choices=[2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=None, choices=[2, 3, 4, 5],
+                    help="run one configuration only (default: configuration 5, then 3, 4 and 2 in the same run)")
     ap.add_argument("--n-mol", type=int, default=343000, help="config 5: water molecules")
     ap.add_argument("--chunk", type=int, default=None, help="receiver chunk (default: 131072; config 3: 16384)")
     ap.add_argument("--graphs", action="store_true", default=None,
@@ -603,16 +673,40 @@ def main():
                     help="after the timed steps, run a plain elementwise kernel over this many MiB (reads and "
                          "writes a buffer of known size: calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     a = ap.parse_args()
+    a.cpu_from = None
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         exit_multi_gpu()
-    if a.config == 5:
+    only = a.config is not None
+    cfg = a.config or 5
+    if cfg == 5:
+        a.config = 5
         a.chunk = a.chunk or 131072
         a.graphs = bool(a.graphs)
         line = run_md(a)
-    elif a.config in (3, 4):
+    elif cfg in (3, 4):
         line = run_ef(a)
     else:
         line = run_conv(a)
+    if not only:
+        # the other configurations in the same process, each with its own roofline and per-kernel table
+        extras = {}
+        cpu5 = line.get("cpu_baseline")
+        for c, steps, warm in ((3, 20, 2), (4, 8, 1), (2, 20, 2)):
+            free_gpu()
+            print(f"# configuration {c}", file=sys.stderr, flush=True)
+            b = argparse.Namespace(**vars(a))
+            b.config, b.steps, b.warmup, b.chunk, b.graphs, b.copy_calib_mib = c, steps, warm, None, None, 0
+            b.no_cpu = True if c == 4 else a.no_cpu
+            b.cpu_from = None
+            if c == 3 and cpu5 is not None:
+                b.cpu_from = dict(cpu5, sample="derived from configuration 5's chunk timing (same water generator, "
+                                               "density and chunk size: the same per-atom CPU work): "
+                                               + cpu5["sample"])
+            extras[f"config{c}"] = sub_line(run_ef(b) if c in (3, 4) else run_conv(b))
+            if c == 4:
+                extras["config4"]["cpu_baseline_note"] = ("not in the default run (bounded run time): "
+                                                          "bench.py --config 4 times one FCC chunk on the CPU")
+        line["configs"] = extras
     print(json.dumps(line), flush=True)
 
 

@@ -2,7 +2,9 @@
 
     python mace-million_amd/build.py            (also called by __graft_entry__.build())
 
-Output: mace-million_amd/lib/libmace_million_amd.so (git-ignored; it travels with the tree to the GPU box).
+Output: mace-million_amd/lib/libmace_million_amd.so (git-ignored; it travels with the tree to the GPU box), and
+lib/kernel_ops.json: the fp32 operations per thread that the straight-line generated symmetric-contraction kernels
+execute, counted from their gfx950 assembly (bench.py reports their FLOP rates from it).
 Every HIP source is compiled with -Xclang -target-feature -Xclang -packed-fp32-ops (no packed-FP32 instructions)
 and -munsafe-fp-atomics (hardware float atomics instead of compare-and-swap loops).
 """
@@ -54,6 +56,27 @@ def _compile(src):
     return obj
 
 
+# straight-line generated kernels whose executed fp32 operations are counted from their gfx950 assembly
+COUNTED = {"symc_l1.hip": ("mm_symc1_fwd_kernel", "mm_symc1_bwd_kernel"),
+           "symc_l2.hip": ("mm_symc2_fwd_kernel", "mm_symc2_bwd_kernel")}
+OPS_JSON = os.path.join(LIB_DIR, "kernel_ops.json")
+
+
+def _count_ops(name):
+    """fp32 VALU operations per thread of the kernels of generated source `name`, from its device assembly."""
+    sys.path.insert(0, HERE)
+    from mace_onegpu import codegen
+
+    src = os.path.join(GEN, name)
+    asm = os.path.join(OBJ, name + ".s")
+    cmd = [HIPCC] + FLAGS + ["--cuda-device-only", "-S", src, "-o", asm]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"assembly failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    text = open(asm).read()
+    return {k: codegen.asm_valu_flops(text, k) for k in COUNTED[name]}
+
+
 def build(jobs=None, verbose=True):
     generate()
     os.makedirs(OBJ, exist_ok=True)
@@ -61,7 +84,14 @@ def build(jobs=None, verbose=True):
     srcs = sources()
     jobs = jobs or min(8, os.cpu_count() or 4)
     with ThreadPoolExecutor(jobs) as ex:
+        counts = [ex.submit(_count_ops, n) for n in COUNTED]
         objs = list(ex.map(_compile, srcs))
+        ops = {}
+        for c in counts:
+            ops.update(c.result())
+    import json
+    with open(OPS_JSON, "w") as fh:
+        json.dump(ops, fh, indent=1)
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -226,6 +226,14 @@ class RefModel:
         self.coupling = coupling
         self.nlayers_r = len(sp.radial_mlp) + 1
 
+    def astype(self, dtype):
+        """A copy whose parameters are held in `dtype` (the fp32 CPU baseline evaluates the same functions)."""
+        import copy
+        m = copy.copy(self)
+        m.P = {k: v.to(dtype) for k, v in self.P.items()}
+        m.e0 = self.e0.to(dtype)
+        return m
+
     def radial_W(self, k):
         return [self.P[f"i{k}_r{j}"] for j in range(self.nlayers_r)]
 
@@ -260,6 +268,13 @@ class Tables64:
             # depend on the species, so every pair holds the same function
             self.TV.append(torch.cat([v0] * (S * S), 0))           # [P*M, D]
             self.TG.append(torch.cat([d * self.h] * (S * S), 0))
+
+    def astype(self, dtype):
+        import copy
+        t = copy.copy(self)
+        t.TV = [v.to(dtype) for v in self.TV]
+        t.TG = [v.to(dtype) for v in self.TG]
+        return t
 
     def lookup(self, k, r, pair):
         """spline_w._w_fwd in fp64: x = clamp((r - r_lo) inv_h, 0, M - 1 - 1e-4), Hermite on [k, k+1]."""
@@ -297,7 +312,7 @@ def layer1_message(m, spec_nodes, nC, send, recv, vec, tables=None, pair=None):
     r, Y, B, f = _edge(m, vec)
     W, d = _weights_density(m, 0, r, B, f, tables, pair)
     W = W.reshape(-1, m.tp1["nW"], C)
-    onehot = torch.nn.functional.one_hot(spec_nodes, m.ne).to(F64)
+    onehot = torch.nn.functional.one_hot(spec_nodes, m.ne).to(m.P["emb"].dtype)
     X = per_l_linear(node_embedding(onehot, m.P["emb"])[:, None, :], [0], m.P["i0_up"], C)
     mji = channelwise_tp(W, X, Y, send, m.tp1["paths"], m.tp1["in_ls"], m.coupling)
     A = scatter_sum(mji, recv, nC)

@@ -49,9 +49,33 @@ def test_symmetric_contraction_flops_closed_forms():
 
 
 def test_published_S1_S2():
-    sf = bench.symc_flops_per_row(_tables())
-    assert sf[(1, "bwd")] == 2 * sf[(1, "fwd")] and sf[(2, "bwd")] == 2 * sf[(2, "fwd")]
-    assert sf[(1, "fwd")] == 915712 and sf[(2, "fwd")] == 129536
+    """The dense-coefficient convention (scripts/flop_budget.py) stays published beside the executed counts."""
+    assert bench.symc_dense_flops(_tables()) == (915712, 129536)
+
+
+def test_written_flops_counter():
+    """fmaf = 2, other binary * and + = 1, += adds 1, 1.0f * is folded; loads, stores and addressing are not
+    counted."""
+    body = """k(int n, const float* x) {
+  const int node = blockIdx.x * 2 + (threadIdx.x >> 7);
+  const float x0 = xp[0];
+  const float z0 = 0.5f * x0 * x1 + -0.25f * x2 * x3;
+  o0 = fmaf(w0, z0, o0);
+  o0 += 1.0f * z0 * x4;
+  gx1 = fmaf(0.7f * q0, x1, gx1);
+  op[0] = o0;
+}"""
+    assert codegen.written_flops(body) == (2 + 1 + 2) + 2 + (1 + 1) + (2 + 1)
+
+
+def test_executed_symc_flops_below_the_dense_count():
+    """The generated kernels evaluate the contractions factorised: fewer operations than the dense convention,
+    and the backward (input gradient plus the density term) more than the forward."""
+    sf = bench.symc_flops_per_row()
+    S1d, S2d = bench.symc_dense_flops(_tables())
+    assert 0 < sf[(1, "fwd")] < S1d and 0 < sf[(2, "fwd")] < S2d
+    assert sf[(1, "bwd")] > sf[(1, "fwd")] and sf[(2, "bwd")] > sf[(2, "fwd")]
+    assert sf[(1, "fwd")] % 128 == 0
 
 
 def test_node_algorithmic_linear_and_symc():
@@ -64,3 +88,20 @@ def test_node_algorithmic_linear_and_symc():
     assert F == rows * 12 and B == 4 * 128 * rows * (16 + 1 + 16) + 12 * rows
     B, F = bench.node_algorithmic("symc1_fwd", (rows,), sf)
     assert F == rows * 10 and B == 4 * 128 * rows * (16 + 4) + 4 * rows
+
+
+def test_build_counts_symc_ops_from_assembly():
+    """The build's assembly count of the straight-line contraction kernels: no packed-FP32 instructions (the build
+    disables them) and somewhat fewer operations than written in the source (the compiler folds multiplications by
+    constants equal to 1 in fp32 and reassociates)."""
+    import pytest
+    ops = os.path.join(ROOT, "mace-million_amd", "lib", "kernel_ops.json")
+    if not os.path.exists(ops):
+        pytest.skip("library not built")
+    gen = os.path.join(ROOT, "mace-million_amd", "csrc", "gen")
+    for layer in (1, 2):
+        asm = codegen.symc_executed_flops(gen, layer, ops_json=ops)
+        src = codegen.symc_executed_flops(gen, layer)
+        for d in ("fwd", "bwd"):
+            assert 0.6 * src[d] <= asm[d] <= src[d], (layer, d, asm[d], src[d])
+    assert all(v["packed"] == 0 for v in json.load(open(ops)).values())
