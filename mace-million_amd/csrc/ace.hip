@@ -12,6 +12,12 @@
 // a wave evaluates edge eb + j of a 64-edge batch into the wave's LDS rows (16 floats per edge), from which the
 // MFMA operands are read (instead of storing and re-reading 64 B of harmonics per edge in global memory).
 //
+// Edge order of the forward: each wave lists its receiver's edges grouped by sender species (mm_ace_group), so that
+// a step of 4 edges holds one species and only that species' MFMAs issue (instead of one MFMA per species with the
+// other species' lanes zeroed).  The backward keeps the CSR order: grouping its 16-edge tiles the same way halved
+// its MFMAs for water but lengthened its per-tile latency chain (order -> edge record -> table rows) and measured
+// slower (2.04 -> 2.17 ms per launch at configuration 5).
+//
 // mm_ace1_fwd: one wave per receiver; B_i accumulated with v_mfma_f32_16x16x4f32 taking 4 edges per step:
 //   A operand (16 q x 4 edges) = ht, lane (i, g) -> q = 16 mt + i of edge g; B operand (4 edges x 16 m) = Y.
 //   Output layout B[i][m][s * 64 + q] (S_pad species blocks, pad species written as 0), rho[i] = sum of the edge
@@ -25,11 +31,59 @@
 
 #define MM_ACE_H 64
 #define MM_ACE_MAX_S 4
-#define MM_ACE_YB 64   // edges per harmonic batch (one per lane)
+#define MM_ACE_YB 64     // slots per harmonic batch (one per lane)
+#define MM_ACE_SEG 240   // edges of one species-grouped segment of a receiver
+#define MM_ACE_SLOTS 256 // slots of a segment's order list: MM_ACE_SEG edges + at most 3 pad slots per species
 
-// lane j: harmonics of edge eb + j (if it exists) into yrow[j * 16 .. + 15]; the edge vector of the next batch is
+// Species-grouped order of the segment [eb, eb + n) of a receiver's edges (n <= MM_ACE_SEG), built by one wave in
+// its LDS list `order`: order[slot] = edge offset within the segment, -1 for a pad slot.  The edges of species s
+// (the sender species, .z of the layer-1 edge record) fill the slots [first[s], first[s + 1]) in their CSR order,
+// and every group starts at a multiple of 4, so a 4-slot step of the forward holds one species: the MFMAs of the
+// other species are skipped.  first[] is wave-uniform.
+template <int S>
+__device__ __forceinline__ void mm_ace_group(const int* __restrict__ pk_i, int eb, int n, int lane,
+                                             int* __restrict__ order, int (&first)[S + 1]) {
+  int slot = 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    first[s] = slot;
+    for (int b = 0; b < n; b += 64) {
+      const int j = b + lane;
+      const bool in = j < n && pk_i[4 * (eb + j) + 2] == s;
+      const unsigned long long mask = __ballot(in);
+      if (in) order[slot + __popcll(mask & ((1ull << lane) - 1ull))] = j;
+      slot += __popcll(mask);
+    }
+    const int pad = (4 - (slot & 3)) & 3;
+    if (lane < pad) order[slot + lane] = -1;
+    slot += pad;
+  }
+  first[S] = slot;
+  mm_wave_lds_sync();
+}
+
+// lane j: harmonics of the edge in slot sb + j (if any) into yrow[j * 16 .. + 15]
+__device__ __forceinline__ void mm_ace_y_batch(int sb, int nslot, int eb, int lane, const int* __restrict__ order,
+                                               const floatx4* __restrict__ e_u, float* __restrict__ yrow) {
+  mm_wave_lds_sync();   // the previous batch has been read
+  const int sl = sb + lane;
+  const int oj = sl < nslot ? order[sl] : -1;
+  if (oj >= 0) {
+    const floatx4 u = e_u[eb + oj];
+    float Y[16];
+    mm_sh16(u.x, u.y, u.z, Y);
+    floatx4* __restrict__ d = (floatx4*)(yrow + lane * 16);
+    d[0] = floatx4{Y[0], Y[1], Y[2], Y[3]};
+    d[1] = floatx4{Y[4], Y[5], Y[6], Y[7]};
+    d[2] = floatx4{Y[8], Y[9], Y[10], Y[11]};
+    d[3] = floatx4{Y[12], Y[13], Y[14], Y[15]};
+  }
+  mm_wave_lds_sync();
+}
+
+// (backward, CSR order) lane j: harmonics of edge eb + j (if it exists) into yrow[j * 16 .. + 15]; the edge vector of the next batch is
 // loaded one batch ahead (u_next)
-__device__ __forceinline__ void mm_ace_y_batch(int eb, int e1, int lane, const floatx4* __restrict__ e_u,
+__device__ __forceinline__ void mm_ace_y_batch_csr(int eb, int e1, int lane, const floatx4* __restrict__ e_u,
                                                floatx4& u_next, float* __restrict__ yrow) {
   mm_wave_lds_sync();   // the previous batch has been read
   const int ej = eb + lane;
@@ -47,6 +101,15 @@ __device__ __forceinline__ void mm_ace_y_batch(int eb, int e1, int lane, const f
   mm_wave_lds_sync();
 }
 
+// species of slot sl (wave-uniform when sl is)
+template <int S>
+__device__ __forceinline__ int mm_ace_species_of(int sl, const int (&first)[S + 1]) {
+  int sp = 0;
+#pragma unroll
+  for (int s = 1; s < S; ++s) sp += sl >= first[s] ? 1 : 0;
+  return __builtin_amdgcn_readfirstlane(sp);
+}
+
 template <int S>
 __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict__ rowptr, int nC,
                                                           const floatx4* __restrict__ e_pk,
@@ -54,44 +117,55 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
                                                           const floatx4* __restrict__ tab, int S_pad,
                                                           float* __restrict__ Bout, float* __restrict__ rho) {
   __shared__ float yrows[4 * MM_ACE_YB * 16];
+  __shared__ int orders[4 * MM_ACE_SLOTS];
   float* __restrict__ yrow = yrows + (threadIdx.x >> 6) * (MM_ACE_YB * 16);
+  int* __restrict__ order = orders + (threadIdx.x >> 6) * MM_ACE_SLOTS;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (i >= nC) return;
+  if (i >= nC) return;   // the kernel synchronises only within a wave
   const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
   const int e0 = rowptr[i], e1 = rowptr[i + 1];
+  const int* __restrict__ pk_i = (const int*)e_pk;
   floatx4 acc[S][4];
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) acc[s][mt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float dsum = 0.f;
-  // the packed record of the next step is loaded one step ahead
-  floatx4 pk_n = e0 + g < e1 ? e_pk[e0 + g] : floatx4{0.f, 0.f, 0.f, 0.f};
-  floatx4 u_next = e0 + lane < e1 ? e_u[e0 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int kb = e0; kb < e1; kb += 4) {
-    if (((kb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch(kb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
-    const int e = kb + g;
-    const bool valid = e < e1;
-    const floatx4 pk = pk_n;
-    const float y = valid ? yrow[((e - e0) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
-    if (e + 4 < e1) pk_n = e_pk[e + 4];
-    const int se = valid ? __float_as_int(pk.z) : -1;
-    const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
-    const float t = pk.x;
-    if (i16 == 0 && valid) dsum += pk.w;
-    // the step's four table rows are loaded together, before any use: an invalid lane reads row 0 (finite) and
-    // its h is zeroed by a factor, so no load sits behind a branch on the edge's validity
-    const float vf = valid ? 1.f : 0.f;
-    floatx4 c[4];
+  for (int eb = e0; eb < e1; eb += MM_ACE_SEG) {
+    const int n = min(MM_ACE_SEG, e1 - eb);
+    int first[S + 1];
+    mm_ace_group<S>(pk_i, eb, n, lane, order, first);
+    const int nslot = first[S];
+    int oj_n = order[g];                                  // the step's slots are read one step ahead
+    floatx4 pk_n = oj_n >= 0 ? e_pk[eb + oj_n] : floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nslot; k += 4) {
+      if ((k & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch(k, nslot, eb, lane, order, e_u, yrow);   // (wave-uniform)
+      const int oj = oj_n;
+      const floatx4 pk = pk_n;
+      if (k + 4 < nslot) {
+        oj_n = order[k + 4 + g];
+        pk_n = oj_n >= 0 ? e_pk[eb + oj_n] : floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+      const bool valid = oj >= 0;
+      const float y = valid ? yrow[((k + g) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
+      const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
+      const float t = pk.x;
+      if (i16 == 0 && valid) dsum += pk.w;
+      // the step's four table rows are loaded together, before any use: a pad lane reads row 0 (finite) and its
+      // h is zeroed by a factor, so no load sits behind a branch on the slot's validity
+      const float vf = valid ? 1.f : 0.f;
+      floatx4 c[4];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) c[mt] = tp[16 * mt];
-    __builtin_amdgcn_sched_barrier(0);
+      for (int mt = 0; mt < 4; ++mt) c[mt] = tp[16 * mt];
+      __builtin_amdgcn_sched_barrier(0);
+      const int sp = mm_ace_species_of<S>(k, first);     // the step's 4 slots hold one species
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const float h = vf * fmaf(fmaf(fmaf(c[mt].w, t, c[mt].z), t, c[mt].y), t, c[mt].x);
+      for (int mt = 0; mt < 4; ++mt) {
+        const float h = vf * fmaf(fmaf(fmaf(c[mt].w, t, c[mt].z), t, c[mt].y), t, c[mt].x);
 #pragma unroll
-      for (int s = 0; s < S; ++s)
-        acc[s][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? h : 0.f, y, acc[s][mt], 0, 0, 0);
+        for (int s = 0; s < S; ++s)
+          if (s == sp) acc[s][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(h, y, acc[s][mt], 0, 0, 0);
+      }
     }
   }
   // C layout: lane (j = i16, g) holds rows 4 g + v (q within the 16-block mt) of column m = j
@@ -132,7 +206,7 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
   floatx4 pk_n = e0 + i16 < e1 ? e_pk[e0 + i16] : floatx4{0.f, 0.f, 0.f, 0.f};
   floatx4 u_next = e0 + lane < e1 ? e_u[e0 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
   for (int tb = e0; tb < e1; tb += 16) {
-    if (((tb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch(tb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
+    if (((tb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch_csr(tb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
     const int e = tb + i16;          // A-operand row: edge i16 of the tile
     const bool valid = e < e1;
     const floatx4 pk = pk_n;

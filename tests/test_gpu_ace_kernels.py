@@ -5,7 +5,8 @@ Semantics checked (the density-projection form of layer 1, reference ace_layer1.
     h_q(e)        = a0 + t (a1 + t (a2 + t a3)),  (a0..a3) = table row of edge e, feature q (64 features)
     B[i, m, s, q] = sum_{e: recv(e) = i, species(e) = s} h_q(e) Y_m(u_e),    rho[i] = sum_e density(e)
     part[e, 1+m]  = sum_q h_q(e) gB[i, m, s_e, q],   part[e, 0] = inv_h sum_m Y_m(u_e) sum_q h'_q(e) gB[i, m, s_e, q]
-Receiver degrees sit at and around the kernels' 64-edge harmonic batches and 16-edge backward tiles.
+Receiver degrees sit at and around the kernels' 64-slot harmonic batches, 16-slot backward tiles and 240-edge
+species-grouped segments.
 """
 import numpy as np
 import pytest
@@ -18,7 +19,7 @@ H = 64
 
 def _case(seed, nC, S, S_pad, NR=11):
     rng = np.random.default_rng(seed)
-    deg = rng.choice([0, 1, 3, 15, 16, 17, 63, 64, 65, 80, 128, 129], nC)
+    deg = rng.choice([0, 1, 3, 15, 16, 17, 63, 64, 65, 80, 128, 129, 239, 240, 241, 300, 481], nC)
     rowptr = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
     E = int(rowptr[-1])
     u = rng.normal(size=(E, 3))
@@ -51,7 +52,7 @@ def _reference(cs):
     return B, rho, dY, dr
 
 
-@pytest.mark.parametrize("S,S_pad", [(2, 2), (3, 4), (4, 4)])
+@pytest.mark.parametrize("S,S_pad", [(1, 2), (2, 2), (3, 4), (4, 4)])
 def test_ace_kernels_against_fp64(S, S_pad):
     from mace_onegpu._lib import K, stream
     assert torch.cuda.is_available(), "GPU test without a GPU"
