@@ -100,6 +100,12 @@ int mm_conv1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u,
 int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                  float* gX, mm_stream_t stream);
+/* Deterministic variant of mm_conv2_bwd (the reference adds dL/dX with tl.atomic_add, conv_spline.py:175-180): the
+ * dL/dX of every edge goes to its own row gXe[e][0:512] instead of atomic adds into gX[send]; mm_gather_rows_csr
+ * then sums the rows per sender in ascending edge order.  Same part[] output. */
+int mm_conv2_bwd_det(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
+                     const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
+                     float* gXe, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- layer-1 ACE form
  * Replace ace_layer1.ACELayer1.message (ace_layer1.py:58-85) and its autograd backward: the exact density-projection
@@ -181,6 +187,11 @@ int mm_ghost_forward(const float* src, float* dst, int D, int nlocal, int nghost
                      mm_stream_t stream);
 int mm_ghost_reverse(const float* src, float* dst, int D, int nlocal, const int* ghost_rowptr, const int* ghost_list,
                      mm_stream_t stream);
+/* dst[r] = sum over j in [rowptr[r], rowptr[r+1]) of src[idx[j]] in ascending j (rows of D floats, D % 4 == 0): the
+ * fixed-order per-sender sum of mm_conv2_bwd_det's rows (G1 = dE2/dh1 gathered as the reference's
+ * G1.index_add_(0, nodes, gh), mliap_threepass.py:547-553, but in a fixed order) */
+int mm_gather_rows_csr(const int* rowptr, const int* idx, const float* src, long src_stride, int D, float* dst,
+                       long dst_stride, int n_rows, mm_stream_t stream);
 /* per-atom forces from pair forces (ReceiverChunkMACE._accum_forces, receiver_chunk_mace.py:272-276) */
 int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* send_rowptr, const long* send_perm,
                             const float* pair_force, double* F, mm_stream_t stream);

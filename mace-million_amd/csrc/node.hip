@@ -227,6 +227,34 @@ extern "C" int mm_ghost_reverse(const float* src, float* dst, int D, int nlocal,
   return mm::launch_status("mm_ghost_reverse");
 }
 
+// ------------------------------------------------------------------------------------------------ row gather
+// dst[r][0:D] = sum over j in [rowptr[r], rowptr[r + 1]) of src[idx[j]][0:D], summed in ascending j by one thread
+// per column (a fixed order: the deterministic reduction of the per-edge dL/dX rows of mm_conv2_bwd_det per
+// sender).  Rows with an empty range are set to 0.  One 64-lane wave per row, float4 columns (D % 4 == 0).
+__global__ void mm_gather_rows_csr_kernel(const int* __restrict__ rowptr, const int* __restrict__ idx,
+                                          const float* __restrict__ src, long src_stride, int D,
+                                          float* __restrict__ dst, long dst_stride, int n_rows) {
+  const long r = (blockIdx.y * (long)gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (r >= n_rows) return;
+  const int lane = threadIdx.x & 63;
+  const int b = rowptr[r], e = rowptr[r + 1];
+  for (int c = 4 * lane; c < D; c += 256) {
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int j = b; j < e; ++j) acc += *(const floatx4*)(src + (long)idx[j] * src_stride + c);
+    *(floatx4*)(dst + r * dst_stride + c) = acc;
+  }
+}
+
+extern "C" int mm_gather_rows_csr(const int* rowptr, const int* idx, const float* src, long src_stride, int D,
+                                  float* dst, long dst_stride, int n_rows, hipStream_t stream) {
+  MM_CHECK_ARG(n_rows >= 0 && D >= 4 && D % 4 == 0 && src_stride % 4 == 0 && dst_stride % 4 == 0 &&
+                   src_stride >= D && dst_stride >= D, "bad sizes (D, strides: multiples of 4, strides >= D)");
+  if (n_rows == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_gather_rows_csr_kernel, rows_grid(((long)n_rows + 3) / 4), dim3(256), 0, stream, rowptr, idx,
+                     src, src_stride, D, dst, dst_stride, n_rows);
+  return mm::launch_status("mm_gather_rows_csr");
+}
+
 // ------------------------------------------------------------------------------------------------ forces
 // F[i] = - sum_{e in row(i)} PF_e + sum_{e : send(e) = i} PF_e with v_e = x_recv - x_send (the reference's
 // _accum_forces, receiver_chunk_mace.py:272-276).  Receiver part: CSR over the receiver-sorted pairs; sender

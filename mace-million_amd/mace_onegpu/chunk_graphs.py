@@ -65,6 +65,9 @@ class _Slot:
         self.lists = torch.zeros(fl.S * nC, **i32)
         self.list_counts = torch.zeros(fl.S, **i32)
         self.PF = torch.zeros(e_cap, 3, **f32)
+        if getattr(fl, "deterministic", False):   # the sender CSR of the deterministic dL/dX sum, real edges only
+            self.sender_rowptr = torch.zeros(n_cap + 1, **i32)
+            self.sender_perm = torch.zeros(e_cap, **i32)
         self.graphs = None
         self.nE = 0
         self.e0 = 0
@@ -76,6 +79,8 @@ class _Slot:
         g.nC, g.nE, g.n_nodes = ex.C, ex.e_cap, ex.n_cap
         g.rowptr, g.ls, g.nodes, g.node_spec = self.rowptr, self.ls, self.nodes, self.node_spec
         g.lists, g.list_counts, g.recompute_lists = self.lists, self.list_counts, recompute_lists
+        if getattr(ex.fl, "deterministic", False):
+            g.sender_rowptr, g.sender_perm = self.sender_rowptr, self.sender_perm
         if ex.mode == "rij":
             g.rij, g.pair_i = self.rij, self.pair_i
         else:
@@ -154,6 +159,13 @@ class ChunkGraphExec:
             s.ls[nE:].fill_(self.n_cap - 1)                 # a pad node: its position is the sink row
             s.recv_local[:nE].copy_(g.recv_local)
             s.recv_local[nE:].fill_(0)
+        if getattr(self.fl, "deterministic", False):   # pad edges are in no sender's range; pad nodes get empty ranges
+            from .fast_layers import sender_csr
+            g.sender_rowptr = None
+            rp, perm = sender_csr(g)
+            s.sender_rowptr[:n + 1].copy_(rp)
+            s.sender_rowptr[n + 1:].fill_(nE)
+            s.sender_perm[:nE].copy_(perm)
         s.nE, s.e0 = nE, g.e0
 
     def check(self, s):

@@ -88,14 +88,32 @@ def comp_of(ls):
     return out, o
 
 
+def sender_csr(g):
+    """(rowptr int32 [n_nodes + 1], edge index int32 [nE]) of chunk g's edges grouped by local sender, ascending edge
+    index within a sender: the fixed summation order of the deterministic sender-feature gradient.  A chunk that
+    carries them (the graph executor's static chunk) is used as is."""
+    if getattr(g, "sender_rowptr", None) is not None:
+        return g.sender_rowptr, g.sender_perm
+    ls = g.ls[:g.nE].long()
+    perm = torch.argsort(ls, stable=True).to(torch.int32)
+    rp = torch.zeros(g.n_nodes + 1, dtype=torch.int32, device=ls.device)
+    rp[1:] = torch.cumsum(torch.bincount(ls, minlength=g.n_nodes), 0).to(torch.int32)
+    return rp, perm
+
+
 class FastLayers:
     """Device constants of the model for a set of present species (model element columns) and the layer pipelines.
 
     species_cols: sorted model element indices present in the system (the reference's `cols`,
     mliap_threepass.py:217); spline_grid: knots M of the radial-weight tables (reference default 512)."""
 
-    def __init__(self, model, species_cols, spline_grid=512, r_lo=0.5, device="cuda", ace_layer1=True):
+    def __init__(self, model, species_cols, spline_grid=512, r_lo=0.5, device="cuda", ace_layer1=True,
+                 deterministic=False):
         self.dev = torch.device(device)
+        # deterministic=True: pass B sums the sender-feature gradient per sender in a fixed order (mm_conv2_bwd_det
+        # + mm_gather_rows_csr) instead of with float atomics, so repeated evaluations are bitwise identical; it
+        # costs a [edges, 512] fp32 buffer per chunk workspace and the per-chunk sender sort
+        self.deterministic = bool(deterministic)
         sp = model.spec
         self.spec = sp
         self.cols = [int(c) for c in species_cols]
@@ -299,6 +317,8 @@ class FastLayers:
         ws = dict(nC=nC, nN=n_nodes, E=E)
         ws.update(e_u=torch.empty(E, 4, **f), e_pk=torch.empty(E, 4, **f),
                   e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
+        if self.deterministic:
+            ws["gXe"] = torch.empty(E, 4 * C, **f)       # per-edge dL/dX rows of mm_conv2_bwd_det
         ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
                   rho=torch.empty(nC, **f), g_rho=torch.empty(nC, **f),
                   M=torch.empty(nC * 16 * C, **f), gM=torch.empty(nC * 16 * C, **f),
@@ -443,10 +463,17 @@ class FastLayers:
                     ws["gM"], 16 * C, ws["rho"], ws["g_rho"], stream())
         self._lin(self.plan_lin2T, ws["gM"], 16 * C, ws["gA"], self.nO2 * C, self.W_lin2T, g.nC, scale=ws["rho"],
                   scale_mode=1)
-        K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
-        self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
-                    ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"], ws["E"] * 17,
-                    ws["gXh"], stream())
+        if self.deterministic:
+            srp, sperm = sender_csr(g)
+            self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd_det, g.rowptr, g.nC, ws["e_pk"],
+                        ws["e_u"], ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
+                        ws["E"] * 17, ws["gXe"], stream())
+            K.mm_gather_rows_csr(srp, sperm, ws["gXe"], D1, D1, ws["gXh"], D1, g.n_nodes, stream())
+        else:
+            K.mm_fill_f32(ws["gXh"], g.n_nodes * D1, 0.0, stream())
+            self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
+                        ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
+                        ws["E"] * 17, ws["gXh"], stream())
         K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
                        PF[g.e0:g.e1], 0, stream())
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)

@@ -124,7 +124,7 @@ def reverse_pairs(sysm):
 
 class MDRunner:
     def __init__(self, model, pos, box, Z, chunk=65536, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device="cuda",
-                 spline_grid=512, use_graphs=False):
+                 spline_grid=512, use_graphs=False, deterministic=None):
         self.model = model
         self.dev = torch.device(device)
         self.r_max = float(model.spec.r_max)
@@ -138,7 +138,7 @@ class MDRunner:
         self.mass = torch.as_tensor(m, dtype=torch.float64, device=self.dev)
         self.gid = torch.arange(len(Z), device=self.dev)       # original atom index of each current slot
         self.ev = ReceiverChunkMACE(model, chunk=chunk, spline_grid=spline_grid, device=self.dev,
-                                    use_graphs=use_graphs)
+                                    use_graphs=use_graphs, deterministic=deterministic)
         self.n_rebuild = 0
         self._build(torch.as_tensor(pos, dtype=torch.float64, device=self.dev))
         self.F = None

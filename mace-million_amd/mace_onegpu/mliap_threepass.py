@@ -105,6 +105,7 @@ class _Knobs:
         self.cap_margin = float(env("MACE3P_CAP_MARGIN", "1.25"))
         self.ace_layer1 = env("MACE3P_ACE_L1", "1") == "1"
         self.check = env("MACE3P_CHECK", "0") == "1"
+        self.deterministic = env("MACE3P_DETERMINISTIC", "0") == "1"
         self.log_path = env("MACE3P_LOG")
 
 
@@ -222,7 +223,7 @@ class _Runtime:
             p.requires_grad_(False)
         plugin.model = model
         self.fl = fast_layers.FastLayers(model, self.cols, spline_grid=plugin.spline_grid, device=dev,
-                                         ace_layer1=k.ace_layer1)
+                                         ace_layer1=k.ace_layer1, deterministic=k.deterministic)
         self.scale, self.shift, self.e0 = self.fl.scale, self.fl.shift, self.fl.e0
         self.D1 = 4 * model.spec.C
         self.chunk = k.chunk or plugin.chunk

@@ -177,10 +177,13 @@ class ReceiverChunkMACE:
     """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
 
     def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True, use_graphs=False,
-                 e_align=65536, ace_layer1=True, check=None):
+                 e_align=65536, ace_layer1=True, check=None, deterministic=None):
         self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
         # host-side range check of every chunk's index arrays before its kernels run (check_chunk)
         self.check = (os.environ.get("MACE3P_CHECK", "0") == "1") if check is None else bool(check)
+        # bitwise-repeatable evaluations (the sender-feature gradient summed in a fixed order, FastLayers)
+        self.deterministic = ((os.environ.get("MACE3P_DETERMINISTIC", "0") == "1") if deterministic is None
+                              else bool(deterministic))
         self.ace_layer1 = bool(ace_layer1)       # layer 1 in the exact density-projection form (csrc/ace.hip)
         self.dev = torch.device(device)
         self.fl = None
@@ -200,7 +203,8 @@ class ReceiverChunkMACE:
             return self.fl          # same species array as the last call: no device-to-host read
         cols = sorted(int(c) for c in torch.unique(sysm.spidx.long()).tolist())
         if self.fl is None or self.fl.cols != cols:
-            self.fl = FastLayers(self.model, cols, self.spline_grid, device=self.dev, ace_layer1=self.ace_layer1)
+            self.fl = FastLayers(self.model, cols, self.spline_grid, device=self.dev, ace_layer1=self.ace_layer1,
+                                 deterministic=self.deterministic)
         self._cols_key = key
         return self.fl
 

@@ -144,3 +144,25 @@ def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local, 
     close("dL/dY", p[:, 1:], gY_r, 1e-5)
     close("inv_h dL/dt", p[:, 0], inv_h * gt_r, 1e-5)
     assert torch.isnan(part[:, E * 17:]).all()      # nothing written past the partials
+
+    # the deterministic variant: per-edge dL/dX rows summed per sender in ascending edge order
+    from mace_onegpu.fast_layers import sender_csr
+    from mace_onegpu.receiver_chunk_mace import ChunkGraph
+    g = ChunkGraph()
+    g.ls, g.nE, g.n_nodes = torch.tensor(cs["send"], dtype=torch.int32, device=dev), E, n_nodes
+    srp, sperm = sender_csr(g)
+    results = []
+    for rep in range(2):
+        part2 = torch.full((8, E * 17 + 5), float("nan"), **f32)
+        gXe = torch.full((max(E, 1), 4 * C), float("nan"), **f32)
+        gX2 = torch.full((n_nodes, 4 * C), float("nan"), **f32)
+        K.mm_conv2_bwd_det(rowptr, nC, pk, eu, X, 4 * C, tab, 1, M, inv_h, gA, part2, E * 17 + 5, gXe, stream())
+        K.mm_gather_rows_csr(srp, sperm, gXe, 4 * C, 4 * C, gX2, 4 * C, n_nodes, stream())
+        torch.cuda.synchronize()
+        results.append((part2.clone(), gX2.clone()))
+    close("gX (deterministic)", gX2, gX_r, 1e-5)
+    assert torch.equal(results[0][1], results[1][1])                # bitwise repeatable
+    assert torch.equal(results[0][0][:, :E * 17], results[1][0][:, :E * 17])
+    p2 = results[0][0][:, :E * 17].view(8, E, 17).double().sum(0).cpu()
+    close("dL/dY (deterministic)", p2[:, 1:], gY_r, 1e-5)
+    close("inv_h dL/dt (deterministic)", p2[:, 0], inv_h * gt_r, 1e-5)
