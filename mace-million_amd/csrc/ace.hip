@@ -182,6 +182,21 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
   if (lane == 0) rho[i] = dsum;
 }
 
+// part rows of the 16-edge tile starting at tb: lane (i16 = m, g) holds dL/dY_m of edges tb + 4 g + v and, in every
+// lane, dL/dr of those edges
+__device__ __forceinline__ void ace_bwd_store(float* __restrict__ part, int tb, int e1, int g, int i16,
+                                              const floatx4& dY, const float (&gr)[4]) {
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int ev = tb + 4 * g + v;
+    if (ev < e1) {
+      float* __restrict__ pp = part + (size_t)ev * 17;
+      pp[1 + i16] = dY[v];
+      if (i16 == 0) pp[0] = gr[v];
+    }
+  }
+}
+
 template <int S>
 __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict__ rowptr, int nC,
                                                           const floatx4* __restrict__ e_pk,
@@ -205,6 +220,9 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
   // the packed record of the next tile is loaded one tile ahead; the tile's harmonics before its MFMAs
   floatx4 pk_n = e0 + i16 < e1 ? e_pk[e0 + i16] : floatx4{0.f, 0.f, 0.f, 0.f};
   floatx4 u_next = e0 + lane < e1 ? e_u[e0 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
+  floatx4 sdY = {0.f, 0.f, 0.f, 0.f};
+  float sgr[4] = {0.f, 0.f, 0.f, 0.f};
+  int stb = -1;
   for (int tb = e0; tb < e1; tb += 16) {
     if (((tb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch_csr(tb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
     const int e = tb + i16;          // A-operand row: edge i16 of the tile
@@ -220,31 +238,34 @@ __global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict_
     const int se = valid ? __float_as_int(pk.z) : -1;
     const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + g;
     const float t = pk.x;
+    // the tile's 16 table rows are loaded together, before any use (one memory latency per tile); a pad lane reads
+    // row 0 (finite) and its A operands are zeroed by the species factors
+    floatx4 c[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) c[k] = tp[4 * k];
+    if (stb >= 0) ace_bwd_store(part, stb, e1, g, i16, sdY, sgr);   // the previous tile's results
+    __builtin_amdgcn_sched_barrier(0);
+    float fs[S];   // 1 for the species of this lane's edge, else 0
+#pragma unroll
+    for (int s = 0; s < S; ++s) fs[s] = se == s ? 1.f : 0.f;
     floatx4 dY = {0.f, 0.f, 0.f, 0.f}, dYp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const floatx4 c = tp[4 * k];
-      const float h = valid ? fmaf(fmaf(fmaf(c.w, t, c.z), t, c.y), t, c.x) : 0.f;
-      const float hp = valid ? fmaf(fmaf(3.f * c.w, t, 2.f * c.z), t, c.y) : 0.f;
+      const float h = fmaf(fmaf(fmaf(c[k].w, t, c[k].z), t, c[k].y), t, c[k].x);
+      const float hp = fmaf(fmaf(3.f * c[k].w, t, 2.f * c[k].z), t, c[k].y);
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        dY = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? h : 0.f, gb[s][k], dY, 0, 0, 0);
-        dYp = __builtin_amdgcn_mfma_f32_16x16x4f32(se == s ? hp : 0.f, gb[s][k], dYp, 0, 0, 0);
+        dY = __builtin_amdgcn_mfma_f32_16x16x4f32(h * fs[s], gb[s][k], dY, 0, 0, 0);
+        dYp = __builtin_amdgcn_mfma_f32_16x16x4f32(hp * fs[s], gb[s][k], dYp, 0, 0, 0);
       }
     }
     // C layout: lane (j = i16 = m, g) holds edges tb + 4 g + v of column m
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int ev = tb + 4 * g + v;
-      const bool ok = ev < e1;
-      const float gr = mm_row_sum16(dYp[v] * yv[v]);
-      if (ok) {
-        float* __restrict__ pp = part + (size_t)ev * 17;
-        pp[1 + i16] = dY[v];
-        if (i16 == 0) pp[0] = gr * inv_h;
-      }
-    }
+    for (int v = 0; v < 4; ++v) sgr[v] = mm_row_sum16(dYp[v] * yv[v]) * inv_h;
+    sdY = dY;
+    stb = tb;
   }
+  if (stb >= 0) ace_bwd_store(part, stb, e1, g, i16, sdY, sgr);
 }
 
 template <int S>
