@@ -57,11 +57,14 @@ int mm_nl_fill(const double* pos_sorted, const int* cell_sorted, long N, const d
 /* per-step pair list of an MD run: pairs of a skin list within r_max (LAMMPS' ML-IAP pair list within the
  * cutoff, inputs/in.water_scan.lmp:44-52) */
 int mm_nl_filter_count(const double* pos, long N, const double* box /* HOST [3] */, const long* skin_rowptr,
-                       const int* skin_send, double r_max2, int* NN, mm_stream_t stream);
+                       const int* skin_send, double r_max2, int* NN,
+                       int* flags /* nullable: per skin pair, 0 if kept else -1 */, mm_stream_t stream);
+/* from_flags != 0: the keep decisions are read from filtered_index, which holds the count pass's flags (no second
+ * distance test); filtered_index is then overwritten with the filtered indices */
 int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] */, const long* skin_rowptr,
                       const int* skin_send, double r_max2, const long* rowptr, int* send,
                       int* filtered_index /* nullable: per skin pair, its index in the filtered list or -1 */,
-                      mm_stream_t stream);
+                      int from_flags, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- edge geometry
  * Replace receiver_chunk_mace.edge_embed (:230-234), the table coordinates of spline_w._coords (spline_w.py:18-27)
@@ -200,6 +203,13 @@ int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* send_rowptr, 
  * reference, whose MD runs inside LAMMPS) */
 int mm_pair_forces_skin(long n, const long* skin_rowptr, const int* filtered_index, const int* rev,
                         const float* pair_force, double* F, mm_stream_t stream);
+/* chunk-local indices of the edges of a receiver-CSR pair list split into receiver chunks of `chunk` receivers:
+ * ls[e] = loc[c * N + send[e]] (sender row in chunk c's node list, loc [n_chunks, N]) and recv_local[e] = i - c *
+ * chunk for receiver i's edges -- the per-chunk ls / receiver arrays of mliap_threepass._topology_all
+ * (mliap_threepass.py:312-331) for every chunk at once, for an MD step whose node lists persist between neighbour
+ * rebuilds */
+int mm_chunk_edge_index(long N, const long* rowptr, const int* send, const int* loc, int chunk, int* ls,
+                        int* recv_local, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- tables
  * conv_spline.build_tables + spline_radial._sample (conv_spline.py:230-249, spline_radial.py:116-151): the radial

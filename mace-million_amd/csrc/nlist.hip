@@ -361,7 +361,11 @@ extern "C" int mm_nl_fill(const double* pos_s, const int* cell_s, long N, const 
 // Per-step pair list of an MD run: the pairs of a skin list (built with r_cut = r_max + skin) whose current
 // minimum-image distance is below r_max, in the skin list's order (the same test as mm_nl_pairs_kernel).
 // One wave per receiver: 64 candidates per step, kept ones compacted in order with a ballot and a prefix popcount.
-template <bool FILL>
+// FILL = false: NN[i] = number of skin pairs of atom i within r_max; with flags != nullptr also flags[e] = 0 (kept)
+// or -1 per skin pair.  FILL = true: the kept pairs in candidate order, send[rowptr[i] + k], and fidx[e] = the
+// filtered index of skin pair e or -1; with FROM_FLAGS the keep decisions are read from fidx (the count pass's
+// flags, written in place) instead of recomputed from the positions.
+template <bool FILL, bool FROM_FLAGS>
 __global__ void __launch_bounds__(256) mm_nl_filter_kernel(const double* __restrict__ pos, long N, double bx,
                                                            double by, double bz, const long* __restrict__ rp_s,
                                                            const int* __restrict__ send_s, double r2,
@@ -370,7 +374,12 @@ __global__ void __launch_bounds__(256) mm_nl_filter_kernel(const double* __restr
   const long i = blockIdx.x * 4L + (threadIdx.x >> 6);
   if (i >= N) return;
   const int lane = threadIdx.x & 63;
-  const double xi = pos[3 * i], yi = pos[3 * i + 1], zi = pos[3 * i + 2];
+  double xi = 0, yi = 0, zi = 0;
+  if (!FROM_FLAGS) {
+    xi = pos[3 * i];
+    yi = pos[3 * i + 1];
+    zi = pos[3 * i + 2];
+  }
   const long end = rp_s[i + 1];
   long n = 0;
   const long base = FILL ? rowptr[i] : 0;
@@ -379,19 +388,25 @@ __global__ void __launch_bounds__(256) mm_nl_filter_kernel(const double* __restr
     bool keep = false;
     int j = 0;
     if (e < end) {
-#pragma clang fp contract(off)
       j = send_s[e];
-      const double dx = mm_mic(xi - pos[3 * (long)j], bx);
-      const double dy = mm_mic(yi - pos[3 * (long)j + 1], by);
-      const double dz = mm_mic(zi - pos[3 * (long)j + 2], bz);
-      const double dd = (dx * dx + dy * dy) + dz * dz;
-      keep = dd < r2 && j != i;
+      if (FROM_FLAGS) {
+        keep = fidx[e] >= 0;
+      } else {
+#pragma clang fp contract(off)
+        const double dx = mm_mic(xi - pos[3 * (long)j], bx);
+        const double dy = mm_mic(yi - pos[3 * (long)j + 1], by);
+        const double dz = mm_mic(zi - pos[3 * (long)j + 2], bz);
+        const double dd = (dx * dx + dy * dy) + dz * dz;
+        keep = dd < r2 && j != i;
+      }
     }
     const unsigned long long m = __ballot(keep);
     if (FILL) {
       const long slot = base + n + __popcll(m & ((1ull << lane) - 1ull));
       if (keep) send[slot] = j;
       if (fidx && e < end) fidx[e] = keep ? (int)slot : -1;
+    } else if (fidx && e < end) {
+      fidx[e] = keep ? 0 : -1;
     }
     n += __popcll(m);
   }
@@ -399,20 +414,25 @@ __global__ void __launch_bounds__(256) mm_nl_filter_kernel(const double* __restr
 }
 
 extern "C" int mm_nl_filter_count(const double* pos, long N, const double* box, const long* rp_s, const int* send_s,
-                                  double r2, int* NN, hipStream_t stream) {
+                                  double r2, int* NN, int* flags, hipStream_t stream) {
   MM_CHECK_ARG(N >= 0 && box, "bad arguments");
   if (N == 0) return MM_OK;
-  hipLaunchKernelGGL(mm_nl_filter_kernel<false>, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, pos, N,
-                     box[0], box[1], box[2], rp_s, send_s, r2, NN, (const long*)nullptr, (int*)nullptr,
-                     (int*)nullptr);
+  hipLaunchKernelGGL((mm_nl_filter_kernel<false, false>), dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, pos,
+                     N, box[0], box[1], box[2], rp_s, send_s, r2, NN, (const long*)nullptr, (int*)nullptr, flags);
   return mm::launch_status("mm_nl_filter_count");
 }
 
 extern "C" int mm_nl_filter_fill(const double* pos, long N, const double* box, const long* rp_s, const int* send_s,
-                                 double r2, const long* rowptr, int* send, int* fidx, hipStream_t stream) {
+                                 double r2, const long* rowptr, int* send, int* fidx, int from_flags,
+                                 hipStream_t stream) {
   MM_CHECK_ARG(N >= 0 && box, "bad arguments");
+  MM_CHECK_ARG(!from_flags || fidx, "from_flags needs the count pass's flags in filtered_index");
   if (N == 0) return MM_OK;
-  hipLaunchKernelGGL(mm_nl_filter_kernel<true>, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, pos, N,
-                     box[0], box[1], box[2], rp_s, send_s, r2, (int*)nullptr, rowptr, send, fidx);
+  if (from_flags)
+    hipLaunchKernelGGL((mm_nl_filter_kernel<true, true>), dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, pos,
+                       N, box[0], box[1], box[2], rp_s, send_s, r2, (int*)nullptr, rowptr, send, fidx);
+  else
+    hipLaunchKernelGGL((mm_nl_filter_kernel<true, false>), dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, pos,
+                       N, box[0], box[1], box[2], rp_s, send_s, r2, (int*)nullptr, rowptr, send, fidx);
   return mm::launch_status("mm_nl_filter_fill");
 }

@@ -332,3 +332,31 @@ extern "C" int mm_pair_forces_skin(long n, const long* skin_rowptr, const int* f
                      fidx, rev, pf, F);
   return mm::launch_status("mm_pair_forces_skin");
 }
+
+// Chunk-local indices of every edge of a receiver-CSR pair list split into receiver chunks [c * chunk, (c + 1) *
+// chunk): ls[e] = loc[c * N + send[e]] (the sender's row in chunk c's node list) and recv_local[e] = i - c * chunk
+// for the edges e of receiver i.  One wave per receiver.
+__global__ void __launch_bounds__(256) mm_chunk_edge_index_kernel(long N, const long* __restrict__ rowptr,
+                                                                  const int* __restrict__ send,
+                                                                  const int* __restrict__ loc, int chunk,
+                                                                  int* __restrict__ ls, int* __restrict__ recv_local) {
+  const long i = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (i >= N) return;
+  const int lane = threadIdx.x & 63;
+  const long c = i / chunk;
+  const int* __restrict__ lc = loc + c * N;
+  const int rl = (int)(i - c * chunk);
+  for (long e = rowptr[i] + lane; e < rowptr[i + 1]; e += 64) {
+    ls[e] = lc[send[e]];
+    recv_local[e] = rl;
+  }
+}
+
+extern "C" int mm_chunk_edge_index(long N, const long* rowptr, const int* send, const int* loc, int chunk, int* ls,
+                                   int* recv_local, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && chunk >= 1, "bad sizes");
+  if (N == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_chunk_edge_index_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, N, rowptr, send,
+                     loc, chunk, ls, recv_local);
+  return mm::launch_status("mm_chunk_edge_index");
+}

@@ -35,8 +35,8 @@ SIGNATURES = {
     "mm_nl_scan": [P, P, L, P, SZ, P],
     "mm_nl_scan_noalloc": [P, P, L, P],
     "mm_nl_fill": [P, P, L, P, P, P, P, D, I, P, P, P],
-    "mm_nl_filter_count": [P, L, P, P, P, D, P, P],
-    "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P, P],
+    "mm_nl_filter_count": [P, L, P, P, P, D, P, P, P],
+    "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P, I, P],
     # geometry
     "mm_edge_geom_rij": [I, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
     "mm_edge_geom_pos": [I, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
@@ -72,6 +72,7 @@ SIGNATURES = {
     "mm_ghost_reverse": [P, P, I, I, P, P, P],
     "mm_pair_forces_to_atoms": [I, P, P, P, P, P, P],
     "mm_pair_forces_skin": [L, P, P, P, P, P, P],
+    "mm_chunk_edge_index": [L, P, P, P, I, P, P, P],
     # tables
     "mm_radial_mlp_f64": [I, P, P, P, P, P, I, I, I, D, I, D, P, P],
     "mm_spline_coeffs": [P, I, I, D, D, I, I, P, P],

@@ -41,13 +41,14 @@ class PairList:
     def refresh(self):
         s = self._skin
         r2 = self.r_max ** 2
-        K.mm_nl_filter_count(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.NN, stream())
+        # the count pass leaves its keep flags in fidx, so the fill pass does not test the distances again
+        K.mm_nl_filter_count(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.NN, self.fidx, stream())
         K.mm_nl_scan(self.NN, self.rowptr, self.N, s._ws, s._ws.numel(), stream())
         self.rp_cpu = self.rowptr.cpu().numpy()          # the one device-to-host read of a step
         E = int(self.rp_cpu[-1])
         if self.send is None or self.send.numel() < E:
             self.send = torch.empty(int(E * 1.1) + 1, dtype=torch.int32, device=self.device)
-        K.mm_nl_filter_fill(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.rowptr, self.send, self.fidx,
+        K.mm_nl_filter_fill(self.pos, self.N, self._box_h, s.rowptr, s.send, r2, self.rowptr, self.send, self.fidx, 1,
                             stream())
         self.E = E
         self.send_view = self.send[:E]
@@ -85,16 +86,19 @@ class PairList:
                 self._tmpl.append(g)
             self._tmpl_key = key
         E = self.E
-        recv = torch.repeat_interleave(torch.arange(N, device=dev, dtype=torch.int32), self.NN, output_size=E)
-        # n_chunks * N < 2^31 for any system this driver holds: int32 flat index into loc
-        ls_all = torch.index_select(self._loc2d.view(-1), 0, (recv // chunk) * N + self.send_view)
+        if getattr(self, "_ls_all", None) is None or self._ls_all.numel() < E:
+            self._ls_all = torch.empty(int(E * 1.1) + 1, dtype=torch.int32, device=dev)
+            self._recv_local = torch.empty_like(self._ls_all)
+        # every chunk's local sender rows and local receivers in one pass over the filtered pairs
+        K.mm_chunk_edge_index(N, self.rowptr, self.send_view, self._loc2d, chunk, self._ls_all, self._recv_local,
+                              stream())
         rp = self.rp_cpu
         for g in self._tmpl:
             e0, e1 = int(rp[g.a]), int(rp[g.b])
             g.e0, g.e1, g.nE = e0, e1, e1 - e0
-            g.ls = ls_all[e0:e1]
+            g.ls = self._ls_all[e0:e1]
             g.rowptr = (self.rowptr[g.a:g.b + 1] - e0).to(torch.int32)
-            g.recv_local = recv[e0:e1] - g.a
+            g.recv_local = self._recv_local[e0:e1]
             g.pos, g.box_host = self.pos, self._box_h
         return self._tmpl
 
