@@ -94,6 +94,8 @@ def _reference(cs, tp):
     ("sparse", 61, 300, 6, False, None),          # few edges, many empty receivers
     # receivers at and around the forward's 64-edge batches of harmonic factors
     ("batch_edges", 67, 1200, 0, False, [1, 3, 4, 5, 63, 64, 65, 127, 128, 129, 192]),
+    # receivers with degrees around multiples of the 4-edge steps and 16-edge groups, in a local sender window
+    ("tile_edges", 71, 900, 0, True, [1, 2, 15, 16, 17, 31, 32, 33, 48, 90]),
 ])
 def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local, degrees):
     from mace_onegpu._lib import K, stream
