@@ -6,8 +6,9 @@
 Prints ONE JSON line.  Default: configuration 5, the metric's "1M-atom water" -- 343,000 rigid H2O molecules
 (1,029,000 atoms) at 1.0 g/cm^3, random-init MPA-0-medium architecture, fp32 kernels, velocity-Verlet MD (dt 0.5 fs,
 300 K Maxwell-Boltzmann start, neighbour skin 2 A, rebuild when an atom moved > 1 A).  One step = one MD step
-(per-step pair filter, energy + forces by the three passes, integration, rebuilds when due).  W untimed steps after
-the initial force call, then K timed steps between synchronisations.
+(per-step pair filter, energy + forces by the three passes with every full receiver chunk replayed from its HIP
+graphs, integration, rebuilds when due; --no-graphs runs every chunk eagerly).  W untimed steps after the initial
+force call, then K timed steps between synchronisations.
   --config 3 : 98,304-atom water, one energy + force evaluation per step (ReceiverChunkMACE, chunk 16384, full chunks
                replayed from HIP graphs), topology of the chunks rebuilt every call
   --config 4 : 500,000-atom FCC Fe/Ni/Cr/Co alloy (a = 3.6 A, sigma 0.05 A), one energy + force evaluation per step
@@ -16,7 +17,7 @@ the initial force call, then K timed steps between synchronisations.
                the layer-2 forward kernel, every kernel listed
 Objects beside the contract fields:
   roofline     : the dominant kernel, algorithmic bytes (or FLOPs) per launch / mean launch time measured with HIP
-                 events on the launch stream during the timed steps.  bound: "valu" for the edge convolutions (fp32
+                 events on the launch stream (during the timed steps; with graphs, in one eager step after them).  bound: "valu" for the edge convolutions (fp32
                  v_fma_f32 on the vector ALUs, roof 157.3 TFLOP/s: gfx950 dual-issues VALU instructions of two waves),
                  "mfma" for the matrix-core kernels, "hbm" below the ridge; traffic = measured HBM bytes per launch
                  from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this workload (or null)
@@ -413,14 +414,25 @@ def run_md(a):
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
     n_pairs = int(md.pairs.E)
+    if a.graphs:
+        # HIP events cannot time launches inside graph replays: one more step with every chunk run eagerly, each
+        # launch timed, gives the per-kernel table (the same kernels the graphs replay)
+        md.ev.use_graphs = False
+        fl.start_kernel_timing()
+        md.step()
+        ktimes = fl.stop_kernel_timing()
+        ksteps = 1
+    else:
+        ksteps = a.steps
     # one more step, after the timed ones, with the linears' and contractions' launches timed as well
     fl.start_kernel_timing(node_kernels=True)
     md.step()
     nodes = node_kernel_table(fl, fl.stop_kernel_timing(), 1)
+    md.ev.use_graphs = a.graphs
     if a.copy_calib_mib > 0:
         copy_calibration(a.copy_calib_mib)
     value = N * a.steps / dt
-    kernels = kernel_table(fl, ktimes, a.steps)
+    kernels = kernel_table(fl, ktimes, ksteps)
     roof = roofline_of(kernels, {"n_mol": a.n_mol, "chunk": a.chunk})
     cpu = None
     if not a.no_cpu:
@@ -435,6 +447,9 @@ def run_md(a):
                       "rebuilds_timed": md.n_rebuild - rebuilds0,
                       "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2),
                       "box_A": round(float(box[0]), 4)}, roof, kernels, cpu)
+    if a.graphs:
+        line["roofline_note"] = ("kernels timed with HIP events in one eager MD step after the graph-replayed timed "
+                                 "steps (events cannot time launches inside a replay)")
     line["node_kernels"] = rounded(nodes)
     line["step_roofline"] = step_roofline(value, n_pairs / N, fl.tables)
     return line
@@ -669,7 +684,7 @@ def main():
     ap.add_argument("--n-mol", type=int, default=343000, help="config 5: water molecules")
     ap.add_argument("--chunk", type=int, default=None, help="receiver chunk (default: 131072; config 3: 16384)")
     ap.add_argument("--graphs", action="store_true", default=None,
-                    help="replay full chunks from HIP graphs (default on for config 3 only)")
+                    help="replay full chunks from HIP graphs (default on for configs 5 and 3)")
     ap.add_argument("--no-graphs", dest="graphs", action="store_false", help="run every chunk eagerly")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
@@ -684,7 +699,7 @@ def main():
     if cfg == 5:
         a.config = 5
         a.chunk = a.chunk or 131072
-        a.graphs = bool(a.graphs)
+        a.graphs = True if a.graphs is None else a.graphs
         line = run_md(a)
     elif cfg in (3, 4):
         line = run_ef(a)

@@ -24,7 +24,7 @@ typedef void* mm_stream_t; /* hipStream_t */
 
 /* ---------------------------------------------------------------------------------------------- library */
 const char* mm_last_error(void);
-/* version of the argument conventions (3); a host binding must refuse a library of another version */
+/* version of the argument conventions (4); a host binding must refuse a library of another version */
 int mm_version(void);
 /* channel count (128), channel blocks (8, one per XCD) and channels per block (16) the kernels were built for */
 int mm_build_info(int* channels, int* channel_blocks, int* block_channels);
@@ -72,20 +72,23 @@ int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] *
  * e_u float4 (unit vector, length; the convolutions and the ACE kernels evaluate Y_lm l<=3 from it), optionally
  * the 16 harmonics e_Y (nullable; the production path passes null), the local receiver, and a packed
  * float4 (t, spline interval row of the ordered species pair's table, sender feature row (its species when
- * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).  dens_w is HOST [nb]. */
-int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* local_send,
-                     const int* node_spec, int S, const int* pair_map, const float* dens_w, int nb, float r_max,
-                     int p_cut, int M, float r_lo, float inv_h, int x_from_spec, float* e_u, float* e_Y /* nullable */,
-                     float* e_pk, int* e_recv, float* e_dd, mm_stream_t stream);
-int mm_edge_geom_pos(int E, const double* pos, const double* box /* HOST [3] */, const int* recv_local, int a,
-                     const int* local_send, const int* nodes, const int* node_spec, int S, const int* pair_map,
-                     const float* dens_w, int nb, float r_max, int p_cut, int M, float r_lo, float inv_h,
-                     int x_from_spec, float* e_u, float* e_Y /* nullable */, float* e_pk, int* e_recv, float* e_dd,
-                     mm_stream_t stream);
+ * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).  dens_w is HOST [nb].  E_dev (nullable): the edge
+ * count read from device memory instead of E, which then only sizes the launch (E_dev <= E; a captured HIP graph
+ * replays a chunk's real count with the grid of its capacity). */
+int mm_edge_geom_rij(int E, const int* E_dev /* nullable */, const double* rij, const int* pair_i, int a,
+                     const int* local_send, const int* node_spec, int S, const int* pair_map, const float* dens_w,
+                     int nb, float r_max, int p_cut, int M, float r_lo, float inv_h, int x_from_spec, float* e_u,
+                     float* e_Y /* nullable */, float* e_pk, int* e_recv, float* e_dd, mm_stream_t stream);
+int mm_edge_geom_pos(int E, const int* E_dev /* nullable */, const double* pos, const double* box /* HOST [3] */,
+                     const int* recv_local, int a, const int* local_send, const int* nodes, const int* node_spec, int S,
+                     const int* pair_map, const float* dens_w, int nb, float r_max, int p_cut, int M, float r_lo,
+                     float inv_h, int x_from_spec, float* e_u, float* e_Y /* nullable */, float* e_pk, int* e_recv,
+                     float* e_dd, mm_stream_t stream);
 /* per-edge dL/dv from the convolution backward partials, the density term and the SH chain rule (the autograd
- * step torch.autograd.grad(..., [vec]) of mliap_threepass.py:550, 580) */
-int mm_edge_grad(int E, const float* part, long part_stride, int n_part, const float* g_rho, const int* e_recv,
-                 const float* e_dd, const float* e_u, float* pair_force, int accumulate, mm_stream_t stream);
+ * step torch.autograd.grad(..., [vec]) of mliap_threepass.py:550, 580); E_dev as for the edge geometry */
+int mm_edge_grad(int E, const int* E_dev /* nullable */, const float* part, long part_stride, int n_part,
+                 const float* g_rho, const int* e_recv, const float* e_dd, const float* e_u, float* pair_force,
+                 int accumulate, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- (2)+(3) edge conv
  * Replace conv_spline.ConvSpline.forward / gen_fwd (conv_spline.py:38-94, 294-301), spline_w._w_fwd
@@ -169,7 +172,10 @@ int mm_symc2_bwd(int n, const float* x, long x_stride, const int* spec, const fl
 /* Equivariant linears on MFMA: linear_up, linear (with / (rho+1)), species-block skip_tp (replaces
  * fast_layers.SpeciesSkip, fast_layers.py:41-105), product linear, and transposes.  comp_* are HOST arrays:
  * nsrc [n_comp], in_off / w_idx [n_comp][3], out_off [n_comp].  W: 128 x 128 weight blocks, each as three bf16
- * planes W0 + W1 + W2 = W (fast_layers.mfma_block); products at fp32 accuracy, fp32 accumulation. */
+ * planes W0 + W1 + W2 = W (fast_layers.mfma_block); products at fp32 accuracy, fp32 accumulation.  Rows: list
+ * (device [n_groups][list_stride]) with list_count (device [n_groups]) selects rows per group; list_count without
+ * list (n_groups 1) reads the row count from device memory, rows 0 .. list_count[0] - 1 (n_rows_max sizes the
+ * launch: a captured HIP graph replays a chunk's real node count). */
 int mm_linear(const float* in, long in_stride, const int* in_rows, float* out, long out_stride, const int* out_rows,
               const void* W, const float* row_scale, int scale_mode, const int* list, const int* list_count,
               long list_stride, int n_groups, int w_group_stride, int n_rows_max, int accumulate, int n_comp,

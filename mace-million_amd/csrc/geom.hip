@@ -92,9 +92,10 @@ __device__ __forceinline__ void mm_geom_common(int e, float vx, float vy, float 
 __global__ void mm_edge_geom_rij_kernel(int E, const double* __restrict__ rij, const int* __restrict__ pair_i, int a,
                                         const int* __restrict__ ls, const int* __restrict__ node_spec, int S,
                                         const int* __restrict__ pair_map, MMDensity dp, MMSpline sp, int x_from_spec,
-                                        float4* e_u, float* e_Y, float4* e_pk, int* e_recv, float* e_dd) {
+                                        float4* e_u, float* e_Y, float4* e_pk, int* e_recv, float* e_dd,
+                                        const int* __restrict__ E_dev) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= E) return;
+  if (e >= (E_dev ? *E_dev : E)) return;   // E_dev: the edge count in device memory (graph replays)
   const float vx = (float)rij[3 * (size_t)e + 0];
   const float vy = (float)rij[3 * (size_t)e + 1];
   const float vz = (float)rij[3 * (size_t)e + 2];
@@ -116,9 +117,9 @@ __global__ void mm_edge_geom_pos_kernel(int E, const double* __restrict__ pos, d
                                         const int* __restrict__ nodes, const int* __restrict__ node_spec, int S,
                                         const int* __restrict__ pair_map, MMDensity dp, MMSpline sp,
                                         int x_from_spec, float4* e_u, float* e_Y, float4* e_pk, int* e_recv,
-                                        float* e_dd) {
+                                        float* e_dd, const int* __restrict__ E_dev) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= E) return;
+  if (e >= (E_dev ? *E_dev : E)) return;   // E_dev: the edge count in device memory (graph replays)
   const int rl = recv_local[e];
   const int sl = ls[e];
   const long gi = nodes[rl], gj = nodes[sl];
@@ -134,9 +135,9 @@ __global__ void mm_edge_geom_pos_kernel(int E, const double* __restrict__ pos, d
 __global__ void mm_edge_grad_kernel(int E, const float* __restrict__ part, long part_stride, int n_part,
                                     const float* __restrict__ g_rho, const int* __restrict__ e_recv,
                                     const float* __restrict__ e_dd, const float4* __restrict__ e_u,
-                                    float* __restrict__ pf, int accumulate) {
+                                    float* __restrict__ pf, int accumulate, const int* __restrict__ E_dev) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= E) return;
+  if (e >= (E_dev ? *E_dev : E)) return;   // E_dev: the edge count in device memory (graph replays)
   float g[17];
 #pragma unroll
   for (int j = 0; j < 17; ++j) g[j] = 0.f;
@@ -176,9 +177,9 @@ static int make_density(MMDensity& dp, const float* w, int nb, float r_max, int 
   return MM_OK;
 }
 
-extern "C" int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int a, const int* ls,
-                                const int* node_spec, int S, const int* pair_map, const float* dens_w, int nb,
-                                float r_max, int p_cut, int M, float r_lo, float inv_h, int x_from_spec,
+extern "C" int mm_edge_geom_rij(int E, const int* E_dev, const double* rij, const int* pair_i, int a,
+                                const int* ls, const int* node_spec, int S, const int* pair_map, const float* dens_w,
+                                int nb, float r_max, int p_cut, int M, float r_lo, float inv_h, int x_from_spec,
                                 float* e_u, float* e_Y, float* e_pk, int* e_recv, float* e_dd, hipStream_t stream) {
   MM_CHECK_ARG(E >= 0 && S >= 1 && M >= 2, "bad sizes");
   MMDensity dp;
@@ -187,15 +188,15 @@ extern "C" int mm_edge_geom_rij(int E, const double* rij, const int* pair_i, int
   if (E == 0) return MM_OK;
   hipLaunchKernelGGL(mm_edge_geom_rij_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, E, rij, pair_i, a, ls,
                      node_spec, S, pair_map, dp, sp, x_from_spec, (float4*)e_u, e_Y, (float4*)e_pk, e_recv,
-                     e_dd);
+                     e_dd, E_dev);
   return mm::launch_status("mm_edge_geom_rij");
 }
 
-extern "C" int mm_edge_geom_pos(int E, const double* pos, const double* box, const int* recv_local, int a,
-                                const int* ls, const int* nodes, const int* node_spec, int S, const int* pair_map,
-                                const float* dens_w, int nb, float r_max, int p_cut, int M, float r_lo,
-                                float inv_h, int x_from_spec, float* e_u, float* e_Y, float* e_pk, int* e_recv,
-                                float* e_dd, hipStream_t stream) {
+extern "C" int mm_edge_geom_pos(int E, const int* E_dev, const double* pos, const double* box,
+                                const int* recv_local, int a, const int* ls, const int* nodes, const int* node_spec,
+                                int S, const int* pair_map, const float* dens_w, int nb, float r_max, int p_cut, int M,
+                                float r_lo, float inv_h, int x_from_spec, float* e_u, float* e_Y, float* e_pk,
+                                int* e_recv, float* e_dd, hipStream_t stream) {
   MM_CHECK_ARG(E >= 0 && S >= 1 && box != nullptr && M >= 2, "bad sizes");
   MMDensity dp;
   MM_CHECK_ARG(make_density(dp, dens_w, nb, r_max, p_cut) == MM_OK, "nb out of range");
@@ -203,16 +204,16 @@ extern "C" int mm_edge_geom_pos(int E, const double* pos, const double* box, con
   if (E == 0) return MM_OK;
   hipLaunchKernelGGL(mm_edge_geom_pos_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, E, pos, box[0], box[1],
                      box[2], recv_local, a, ls, nodes, node_spec, S, pair_map, dp, sp, x_from_spec, (float4*)e_u,
-                     e_Y, (float4*)e_pk, e_recv, e_dd);
+                     e_Y, (float4*)e_pk, e_recv, e_dd, E_dev);
   return mm::launch_status("mm_edge_geom_pos");
 }
 
-extern "C" int mm_edge_grad(int E, const float* part, long part_stride, int n_part, const float* g_rho,
-                            const int* e_recv, const float* e_dd, const float* e_u, float* pf, int accumulate,
-                            hipStream_t stream) {
+extern "C" int mm_edge_grad(int E, const int* E_dev, const float* part, long part_stride, int n_part,
+                            const float* g_rho, const int* e_recv, const float* e_dd, const float* e_u, float* pf,
+                            int accumulate, hipStream_t stream) {
   MM_CHECK_ARG(E >= 0 && n_part >= 0, "bad sizes");
   if (E == 0) return MM_OK;
   hipLaunchKernelGGL(mm_edge_grad_kernel, dim3((E + 255) / 256), dim3(256), 0, stream, E, part, part_stride, n_part,
-                     g_rho, e_recv, e_dd, (const float4*)e_u, pf, accumulate);
+                     g_rho, e_recv, e_dd, (const float4*)e_u, pf, accumulate, E_dev);
   return mm::launch_status("mm_edge_grad");
 }

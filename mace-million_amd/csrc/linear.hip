@@ -56,7 +56,7 @@ struct MMLinArgs {
   const float* row_scale; // nullable: per logical row id
   int scale_mode;         // 0: scale = row_scale[id]; 1: scale = 1 / (row_scale[id] + 1)
   const int* list;        // nullable: per group g, list[g * list_stride + r] = logical row id
-  const int* list_count;  // per group row count (device), with list
+  const int* list_count;  // per group row count (device): with list, or alone for one group of rows 0 .. n - 1
   long list_stride;
   int n_rows;             // without list
   int w_group_stride;     // weight block offset of group g (species)
@@ -104,7 +104,7 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
   __shared__ uint4 Wl[3 * 2048];
   const MMLinComp& cp = args.comp[blockIdx.x];   // kernel-argument memory, read with uniform indices
   const int grp = blockIdx.z;
-  const int nrows = args.list ? args.list_count[grp] : args.n_rows;
+  const int nrows = args.list_count ? min(args.list_count[grp], args.n_rows) : args.n_rows;
   const int blk0 = blockIdx.y * n_blk;
   if (blk0 * MM_LIN_BLOCK_ROWS >= nrows) return;
   const int blk1 = min(blk0 + n_blk, (nrows + MM_LIN_BLOCK_ROWS - 1) / MM_LIN_BLOCK_ROWS);
@@ -202,7 +202,9 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
                          const int* comp_w_idx, const int* comp_out_off, hipStream_t stream) {
   MM_CHECK_ARG(n_comp >= 1 && n_comp <= MM_LIN_MAX_COMP, "n_comp out of range");
   MM_CHECK_ARG(n_groups >= 1 && n_rows_max >= 0, "bad sizes");
-  MM_CHECK_ARG((list == nullptr) == (list_count == nullptr), "list and list_count go together");
+  MM_CHECK_ARG(list == nullptr || list_count != nullptr, "a row list needs its counts");
+  MM_CHECK_ARG(list != nullptr || list_count == nullptr || n_groups == 1, "a device row count without a list is for "
+               "one group");
   MM_CHECK_ARG(list != nullptr || n_groups == 1, "groups need row lists");
   MM_CHECK_ARG(in_stride % 4 == 0, "input row stride must be a multiple of 4 floats");
   MMLinArgs a;

@@ -11,7 +11,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libmace_million_amd.so")
-ABI_VERSION = 3     # mm_version() of the library this binding's buffer layouts are written for
+ABI_VERSION = 4     # mm_version() of the library this binding's buffer layouts are written for
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -38,13 +38,13 @@ SIGNATURES = {
     "mm_nl_filter_count": [P, L, P, P, P, D, P, P, P],
     "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P, I, P],
     # geometry
-    "mm_edge_geom_rij": [I, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
-    "mm_edge_geom_pos": [I, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
+    "mm_edge_geom_rij": [I, P, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
+    "mm_edge_geom_pos": [I, P, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
     # layer-1 ACE kernels
     "mm_ace1_fwd": [P, I, P, P, P, I, I, P, P, P],
     "mm_ace1_bwd": [P, I, P, P, P, I, I, P, F, P, P],
     "mm_spline_coeffs_flat": [P, I, I, D, D, I, P, P],
-    "mm_edge_grad": [I, P, L, I, P, P, P, P, P, I, P],
+    "mm_edge_grad": [I, P, P, L, I, P, P, P, P, P, I, P],
     # convolutions (generated)
     "mm_conv1_fwd": [P, I, P, P, P, I, P, I, I, P, P, P],
     "mm_conv2_fwd": [P, I, P, P, P, I, P, I, I, P, P, P],

@@ -17,12 +17,15 @@ The arithmetic is the eager path's (FastLayers.pass_a/b/c run on a static ChunkG
 the eager path up to the order of the fp32 atomic additions of the sender-feature gradient.
 
 Padding:
-* Edges beyond a chunk's nE are outside every receiver's CSR range, so no convolution reads them. Their
-  geometry is computed from harmless inputs: in the LAMMPS path rij = (1.5 r_max, 0, 0) with receiver 0; in the
-  standalone path the sender is a pad node.
+* The captured launches are sized for the capacities, but the per-edge kernels (geometry, pair-force assembly)
+  read the chunk's edge count from its CSR end (rowptr[nC], device memory) and the node-level linears the node
+  count from the slot's device counter: a replay does the loaded chunk's own work.
+* Edges beyond a chunk's nE are outside every receiver's CSR range, so no convolution reads them. They hold
+  harmless inputs: in the LAMMPS path rij = (1.5 r_max, 0, 0) with receiver 0; in the standalone path the sender is
+  a pad node.
 * Nodes beyond the chunk's n_nodes point at a sink row (index nt_cap) of the static H1x / G1 / position
-  buffers. H1x[sink] = 0, and the G1 scatter of pad rows lands in G1[sink], never in a real atom's row.
-* Species lists are rebuilt in pass A's graph only; passes B and C reuse them.
+  buffers. H1x[sink] = 0, and a G1 scatter of pad rows would land in G1[sink], never in a real atom's row.
+* The per-species receiver lists are loaded with the topology (built once per chunk object, outside the graphs).
 
 Partial chunks run eagerly on the same buffers.  Buffers are cleared inside graphs with fill kernels only.
 """
@@ -65,6 +68,7 @@ class _Slot:
         self.lists = torch.zeros(fl.S * nC, **i32)
         self.list_counts = torch.zeros(fl.S, **i32)
         self.PF = torch.zeros(e_cap, 3, **f32)
+        self.n_nodes_dev = torch.zeros(1, **i32)   # the loaded chunk's node count (its edge count is rowptr[nC])
         if getattr(fl, "deterministic", False):   # the sender CSR of the deterministic dL/dX sum, real edges only
             self.sender_rowptr = torch.zeros(n_cap + 1, **i32)
             self.sender_perm = torch.zeros(e_cap, **i32)
@@ -72,13 +76,16 @@ class _Slot:
         self.nE = 0
         self.e0 = 0
 
-    def chunk(self, ex, recompute_lists):
+    def chunk(self, ex):
         """The static ChunkGraph the captured passes run on (PF offsets index the slot's own PF buffer)."""
         g = ChunkGraph()
         g.a, g.b, g.e0, g.e1 = self.a, self.b, 0, ex.e_cap
         g.nC, g.nE, g.n_nodes = ex.C, ex.e_cap, ex.n_cap
         g.rowptr, g.ls, g.nodes, g.node_spec = self.rowptr, self.ls, self.nodes, self.node_spec
-        g.lists, g.list_counts, g.recompute_lists = self.lists, self.list_counts, recompute_lists
+        g.lists, g.list_counts = self.lists, self.list_counts
+        # the edge and node kernels read the loaded chunk's counts from device memory, so a replay does the
+        # chunk's own work, not the capacities' (the grids are sized for the capacities)
+        g.E_dev, g.N_dev = self.rowptr[ex.C:], self.n_nodes_dev
         if getattr(ex.fl, "deterministic", False):
             g.sender_rowptr, g.sender_perm = self.sender_rowptr, self.sender_perm
         if ex.mode == "rij":
@@ -147,7 +154,16 @@ class ChunkGraphExec:
         s.nodes[n:].fill_(self.sink)
         s.node_spec[:n].copy_(g.node_spec)
         s.node_spec[n:].fill_(0)
+        # the per-species receiver lists, built once per chunk object (as the eager path keeps them) and copied in
+        if getattr(g, "lists", None) is None:
+            fl = self.fl
+            g.lists = torch.empty(fl.S * g.nC, dtype=torch.int32, device=fl.dev)
+            g.list_counts = torch.empty(fl.S, dtype=torch.int32, device=fl.dev)
+            K.mm_species_lists(g.node_spec, g.nC, fl.S, g.lists, g.nC, g.list_counts, stream())
+        s.lists.copy_(g.lists)
+        s.list_counts.copy_(g.list_counts)
         s.rowptr.copy_(g.rowptr)
+        s.n_nodes_dev.fill_(n)
         s.ls[:nE].copy_(g.ls)
         if self.mode == "rij":
             s.ls[nE:].fill_(0)
@@ -213,13 +229,13 @@ class ChunkGraphExec:
 
     # ------------------------------------------------------------------ captured bodies
     def _body_A(self, s):
-        self.fl.pass_a(s.chunk(self, True), self.H1, self.cache())
+        self.fl.pass_a(s.chunk(self), self.H1, self.cache())
 
     def _body_B(self, s):
-        self.fl.pass_b(s.chunk(self, False), self.H1x, self.G1, s.PF, self.eat)
+        self.fl.pass_b(s.chunk(self), self.H1x, self.G1, s.PF, self.eat)
 
     def _body_C(self, s):
-        g = s.chunk(self, False)
+        g = s.chunk(self)
         if self.cache_layer1:
             self.fl.pass_c(g, self.G1r, s.PF, self.eat, self.H1x, self.cache())
         else:

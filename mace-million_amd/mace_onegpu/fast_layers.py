@@ -330,7 +330,8 @@ class FastLayers:
 
     # ------------------------------------------------------------------ helpers
     def _lin(self, plan, inp, in_stride, out, out_stride, W, rows, in_rows=None, out_rows=None, scale=None,
-             scale_mode=0, species=False, accumulate=0, w_group_stride=0):
+             scale_mode=0, species=False, accumulate=0, w_group_stride=0, count_dev=None):
+        """count_dev (optional device int32 [1]): the row count read by the kernel, rows only sizing the launch."""
         ws = self.ws
         units = (rows, plan.k_sum, plan.n_in, plan.n, accumulate, plan.n_w * (self.S if species else 1))
         if species:
@@ -339,8 +340,8 @@ class FastLayers:
                         accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, stream())
         else:
             self._timed("linear", units, K.mm_linear, inp, in_stride, in_rows, out, out_stride, out_rows, W, scale,
-                        scale_mode, None, None, 0, 1, 0, rows, accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx,
-                        plan.outoff, stream())
+                        scale_mode, None, count_dev, 0, 1, 0, rows, accumulate, plan.n, plan.nsrc, plan.inoff,
+                        plan.widx, plan.outoff, stream())
 
     def _geometry(self, k, g):
         """Edge geometry of chunk g for interaction block k (LAMMPS pair vectors or positions)."""
@@ -348,11 +349,11 @@ class FastLayers:
         sp = self.spec
         x_from_spec = 1 if k == 0 else 0          # layer-1 sender features depend on the species only
         if g.rij is not None:
-            K.mm_edge_geom_rij(g.nE, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
+            K.mm_edge_geom_rij(g.nE, g.E_dev, g.rij, g.pair_i, g.a, g.ls, ws["spec"], self.S, self.pair_map, self.dens[k],
                                sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo, self.inv_h, x_from_spec,
                                ws["e_u"], None, ws["e_pk"], ws["e_recv"], ws["e_dd"], stream())
         else:
-            K.mm_edge_geom_pos(g.nE, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
+            K.mm_edge_geom_pos(g.nE, g.E_dev, g.pos, g.box_host, g.recv_local, g.a, g.ls, g.nodes, ws["spec"], self.S,
                                self.pair_map, self.dens[k], sp.num_bessel, sp.r_max, sp.p_cutoff, self.M, self.r_lo,
                                self.inv_h, x_from_spec, ws["e_u"], None, ws["e_pk"], ws["e_recv"],
                                ws["e_dd"], stream())
@@ -361,13 +362,11 @@ class FastLayers:
         """Per-chunk node species and per-species receiver lists (g.node_spec: compact species of local nodes)."""
         ws = self.workspace(g.nC, g.n_nodes, g.nE)
         ws["spec"] = g.node_spec
-        # per-species receiver lists of the chunk: built once per chunk object and shared by the three passes
-        # (a chunk marked recompute_lists -- the static chunk of the HIP-graph executor -- rebuilds them in place)
+        # per-species receiver lists of the chunk: built once per chunk object and shared by the three passes (the
+        # HIP-graph executor loads them into its static chunk with the topology)
         if getattr(g, "lists", None) is None:
             g.lists = torch.empty(self.S * g.nC, dtype=torch.int32, device=self.dev)
             g.list_counts = torch.empty(self.S, dtype=torch.int32, device=self.dev)
-            K.mm_species_lists(g.node_spec, g.nC, self.S, g.lists, g.nC, g.list_counts, stream())
-        elif getattr(g, "recompute_lists", False):
             K.mm_species_lists(g.node_spec, g.nC, self.S, g.lists, g.nC, g.list_counts, stream())
         ws["lists"], ws["counts"], ws["lists_stride"] = g.lists, g.list_counts, g.nC
         return ws
@@ -433,7 +432,7 @@ class FastLayers:
                         ws["e_u"], self.Xs1, C, self.tab[0], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
                         ws["E"] * 17, None, stream())
             n_part = NCB
-        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, n_part, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
+        K.mm_edge_grad(g.nE, g.E_dev, ws["part"], ws["E"] * 17, n_part, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
                        PF[g.e0:g.e1], 1, stream())
 
     # ------------------------------------------------------------------ layer 2
@@ -446,7 +445,7 @@ class FastLayers:
         # sc = skip_tp(h1_recv) per species (0e part only), written into h2; the receivers are g.nodes[:nC]
         self._lin(self.plan_sk1, H1x, D1, h2, C, self.W_sk1, g.nC, in_rows=g.nodes, species=True, w_group_stride=1)
         # node features of every local node: linear_up(H1x[nodes])
-        self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes)
+        self._lin(self.plan_p1, H1x, D1, ws["Xh"], D1, self.W_up2, g.n_nodes, in_rows=g.nodes, count_dev=g.N_dev)
         self._geometry(1, g)
         self._timed("conv2_fwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_fwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                     ws["Xh"], D1, self.tab[1], self.n_tab, self.M, ws["A"], ws["rho"], stream())
@@ -474,8 +473,9 @@ class FastLayers:
             self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                         ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
                         ws["E"] * 17, ws["gXh"], stream())
-        K.mm_edge_grad(g.nE, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
+        K.mm_edge_grad(g.nE, g.E_dev, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
                        PF[g.e0:g.e1], 0, stream())
-        self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1)
+        self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1,
+                  count_dev=g.N_dev)
         self._lin(self.plan_sk1, gh2, C, G1, D1, self.W_sk1T, g.nC, out_rows=g.nodes, species=True, w_group_stride=1,
                   accumulate=1)

@@ -102,6 +102,8 @@ class ChunkGraph:
     pos = None
     box_host = None
     recv_local = None
+    E_dev = None   # device int32 [1]: the edge count the edge kernels read (graph replays); None: nE
+    N_dev = None   # device int32 [1]: the node count of the node-level linears (graph replays); None: n_nodes
 
 
 def chunk_topology(a, b, e0, e1, pj, loc, flag):

@@ -37,6 +37,15 @@ def _chunks(mode, nC=8, n_chunks=3, seed=0):
         loc = {int(v): i for i, v in enumerate(g.nodes)}
         g.ls = torch.tensor([loc[int(v)] for v in send[e0:e1]], dtype=torch.int32)
         g.node_spec = (g.nodes % 2).int()
+        # per-species receiver lists as mm_species_lists builds them (stable partition, stride nC); a slot load
+        # copies them (the production callers build them on the GPU, once per chunk object)
+        spec_r = g.node_spec[:nC].long()
+        g.lists = torch.zeros(2 * nC, dtype=torch.int32)
+        g.list_counts = torch.zeros(2, dtype=torch.int32)
+        for sp in range(2):
+            idx = torch.nonzero(spec_r == sp).squeeze(1).int()
+            g.lists[sp * nC: sp * nC + len(idx)] = idx
+            g.list_counts[sp] = len(idx)
         g.rowptr = (rp[a:b + 1] - e0).int()
         if mode == "rij":
             g.pair_i = recv[e0:e1].int()
@@ -57,6 +66,7 @@ def test_loaded_slots_index_inside_their_buffers(mode):
         s = ex.slots[g.a // 8] = chunk_graphs._Slot(ex, g.a // 8)
         ex._load(s, g)
         ex.check(s)
+        assert torch.equal(s.lists, g.lists) and torch.equal(s.list_counts, g.list_counts)
         if mode == "rij":     # what the kernel computes: pair_i - a, for real and pad edges
             recv = s.pair_i.long() - s.a
             assert torch.equal(recv[:g.nE], g.pair_i.long() - g.a) and bool((recv[g.nE:] == 0).all())

@@ -46,11 +46,23 @@ def test_edge_grad_against_fp64_autograd(n_part, accumulate):
     eu[:, 3] = r.float().to(dev)
     pd = part.float().to(dev).contiguous()
     pf = pf0.float().to(dev).contiguous() if accumulate else torch.full((E, 3), float("nan"), device=dev)
-    K.mm_edge_grad(E, pd, E * 17, n_part, g_rho.float().to(dev), recv.to(torch.int32).to(dev), dd.float().to(dev),
-                   eu, pf, accumulate, stream())
+    K.mm_edge_grad(E, None, pd, E * 17, n_part, g_rho.float().to(dev), recv.to(torch.int32).to(dev),
+                   dd.float().to(dev), eu, pf, accumulate, stream())
     torch.cuda.synchronize()
     got = pf.double().cpu()
     err = float((got - ref).abs().max())
     scale = float(ref.abs().max())
     print(f"  pf: max|err| {err:.3e} (max|ref| {scale:.3e})", flush=True)
     assert torch.isfinite(got).all() and err <= 1e-5 * scale
+
+    # the edge count from device memory (graph replays): a launch sized for E processes only the first E_dev edges
+    E_real = E - 357
+    pf2 = pf0.float().to(dev).contiguous() if accumulate else torch.full((E, 3), float("nan"), device=dev)
+    before = pf2.clone()
+    K.mm_edge_grad(E, torch.tensor([E_real], dtype=torch.int32, device=dev), pd, E * 17, n_part,
+                   g_rho.float().to(dev), recv.to(torch.int32).to(dev), dd.float().to(dev), eu, pf2, accumulate,
+                   stream())
+    torch.cuda.synchronize()
+    assert torch.equal(pf2[:E_real], pf[:E_real])                       # the same kernel arithmetic
+    assert torch.equal(pf2[E_real:].isnan(), before[E_real:].isnan())   # nothing beyond E_dev written
+    assert torch.equal(torch.nan_to_num(pf2[E_real:]), torch.nan_to_num(before[E_real:]))

@@ -57,10 +57,18 @@ def test_edge_geometry_against_fp64(x_from_spec):
     e_recv = torch.full((E,), -7, **i32)
     e_dd = torch.full((E,), float("nan"), device=dev)
     dens_w = (ctypes.c_float * nb)(*w.tolist())
-    K.mm_edge_geom_rij(E, rij.to(dev), (recv + a).to(**i32), a, send.to(**i32), spec.to(**i32), S,
+    K.mm_edge_geom_rij(E, None, rij.to(dev), (recv + a).to(**i32), a, send.to(**i32), spec.to(**i32), S,
                        pair_map.to(**i32), dens_w, nb, r_max, p, M, r_lo, 1.0 / h, x_from_spec, e_u, None, e_pk,
                        e_recv, e_dd, stream())
+    # the edge count from device memory (graph replays): the same launch writes only the first E_dev edges
+    E_real = E // 3
+    pk2 = torch.full((E, 4), float("nan"), device=dev)
+    K.mm_edge_geom_rij(E, torch.tensor([E_real], **i32), rij.to(dev), (recv + a).to(**i32), a, send.to(**i32),
+                       spec.to(**i32), S, pair_map.to(**i32), dens_w, nb, r_max, p, M, r_lo, 1.0 / h, x_from_spec,
+                       torch.empty_like(e_u), None, pk2, torch.empty_like(e_recv), torch.empty_like(e_dd), stream())
     torch.cuda.synchronize()
+    assert torch.equal(pk2[:E_real].view(torch.int32), e_pk[:E_real].view(torch.int32))
+    assert bool(pk2[E_real:].isnan().all())
     e_u, e_pk, e_recv, e_dd = e_u.cpu().double(), e_pk.cpu(), e_recv.cpu(), e_dd.cpu().double()
     pki = e_pk.view(torch.int32)
 
@@ -100,7 +108,7 @@ def test_spline_interval_stays_inside_the_table(M):
     e_recv = torch.empty(E, **i32)
     e_dd = torch.empty(E, device=dev)
     dens_w = (ctypes.c_float * nb)(*([0.1] * nb))
-    K.mm_edge_geom_rij(E, rij.to(dev), torch.zeros(E, **i32), 0, torch.zeros(E, **i32), torch.zeros(1, **i32), S,
+    K.mm_edge_geom_rij(E, None, rij.to(dev), torch.zeros(E, **i32), 0, torch.zeros(E, **i32), torch.zeros(1, **i32), S,
                        torch.zeros(1, **i32), dens_w, nb, r_max, p, M, r_lo, 1.0 / h, 0, e_u, None, e_pk, e_recv,
                        e_dd, stream())
     torch.cuda.synchronize()

@@ -145,6 +145,21 @@ def test_mfma_linear_against_torch(dev):
     for s in range(S):
         c = int(counts[s])
         assert torch.equal(lists[s, :c].cpu().long(), torch.nonzero(spec == s).squeeze(1))
+    # the row count from device memory (graph replays): a launch sized for n rows computes rows 0 .. n_dev - 1
+    # only, bit for bit as a launch of n_dev rows, and leaves the rest untouched
+    n_dev = 150
+    xs = x[:, :128].float().to(dev).contiguous()
+    p1 = LinPlan([(0, [(0, 0)])])
+    a = torch.full((n, 128), float("nan"), device=dev)
+    b = torch.full((n, 128), float("nan"), device=dev)
+    _lib.K.mm_linear(xs, 128, None, a, 128, None, W, None, 0, None, None, 0, 1, 0, n_dev, 0, p1.n, p1.nsrc,
+                     p1.inoff, p1.widx, p1.outoff, _lib.stream())
+    _lib.K.mm_linear(xs, 128, None, b, 128, None, W, None, 0, None,
+                     torch.tensor([n_dev], dtype=torch.int32, device=dev), 0, 1, 0, n, 0, p1.n, p1.nsrc, p1.inoff,
+                     p1.widx, p1.outoff, _lib.stream())
+    torch.cuda.synchronize()
+    assert torch.equal(a[:n_dev], b[:n_dev]) and bool(torch.isfinite(b[:n_dev]).all())
+    assert bool(b[n_dev:].isnan().all())
 
 
 def test_spline_tables_against_oracle_hermite(dev, model, ref_model):
