@@ -73,6 +73,7 @@ class _Slot:
             self.sender_rowptr = torch.zeros(n_cap + 1, **i32)
             self.sender_perm = torch.zeros(e_cap, **i32)
         self.graphs = None
+        self.node_src, self.node_key, self.loaded = None, None, False
         self.nE = 0
         self.e0 = 0
 
@@ -150,31 +151,46 @@ class ChunkGraphExec:
                              f"capacities ({self.C}, {self.n_cap - 1}, {self.e_cap})")
         if g.a != s.a:
             raise ValueError(f"chunk starting at receiver {g.a} loaded into the slot of receiver {s.a}")
-        s.nodes[:n].copy_(g.nodes)
-        s.nodes[n:].fill_(self.sink)
-        s.node_spec[:n].copy_(g.node_spec)
-        s.node_spec[n:].fill_(0)
-        # the per-species receiver lists, built once per chunk object (as the eager path keeps them) and copied in
+        # the per-species receiver lists, built once per chunk object (as the eager path keeps them)
         if getattr(g, "lists", None) is None:
             fl = self.fl
             g.lists = torch.empty(fl.S * g.nC, dtype=torch.int32, device=fl.dev)
             g.list_counts = torch.empty(fl.S, dtype=torch.int32, device=fl.dev)
             K.mm_species_lists(g.node_spec, g.nC, fl.S, g.lists, g.nC, g.list_counts, stream())
-        s.lists.copy_(g.lists)
-        s.list_counts.copy_(g.list_counts)
+        # the node set (nodes, species, lists) changes only with the chunk object or an in-place write to one of its
+        # tensors: MD keeps its chunk objects until a neighbour-list rebuild, so most calls load edges only.  The
+        # slot holds references to the tensors it copied (so that they stay the same objects) and their versions.
+        src = (g.nodes, g.node_spec, g.lists, g.list_counts)
+        key = tuple(t._version for t in src)
+        same = s.node_src is not None and all(a is b for a, b in zip(s.node_src, src)) and s.node_key == key
+        if not same:
+            s.nodes[:n].copy_(g.nodes)
+            s.nodes[n:].fill_(self.sink)
+            s.node_spec[:n].copy_(g.node_spec)
+            s.node_spec[n:].fill_(0)
+            s.lists.copy_(g.lists)
+            s.list_counts.copy_(g.list_counts)
+            s.n_nodes_dev.fill_(n)
+            s.node_src, s.node_key = src, key
         s.rowptr.copy_(g.rowptr)
-        s.n_nodes_dev.fill_(n)
         s.ls[:nE].copy_(g.ls)
+        # edges beyond nE are read by no kernel (the edge kernels stop at the device count rowptr[nC], the
+        # convolutions at each receiver's CSR range); they are given harmless values at the slot's first load and
+        # otherwise keep those of an earlier load, which are valid indices as well
+        first = not s.loaded
         if self.mode == "rij":
-            s.ls[nE:].fill_(0)
             s.rij[:nE].copy_(g.rij)
-            s.rij[nE:].copy_(self.pad_rij.expand(self.e_cap - nE, 3))
             s.pair_i[:nE].copy_(g.pair_i)                   # global receivers, as the eager chunk has them
-            s.pair_i[nE:].fill_(s.a)
+            if first:
+                s.ls[nE:].fill_(0)
+                s.rij[nE:].copy_(self.pad_rij.expand(self.e_cap - nE, 3))
+                s.pair_i[nE:].fill_(s.a)
         else:
-            s.ls[nE:].fill_(self.n_cap - 1)                 # a pad node: its position is the sink row
             s.recv_local[:nE].copy_(g.recv_local)
-            s.recv_local[nE:].fill_(0)
+            if first:
+                s.ls[nE:].fill_(self.n_cap - 1)             # a pad node: its position is the sink row
+                s.recv_local[nE:].fill_(0)
+        s.loaded = True
         if getattr(self.fl, "deterministic", False):   # pad edges are in no sender's range; pad nodes get empty ranges
             from .fast_layers import sender_csr
             g.sender_rowptr = None

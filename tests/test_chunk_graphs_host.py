@@ -96,3 +96,31 @@ def test_load_rejects_a_chunk_of_another_slot():
     s = chunk_graphs._Slot(ex, 0)
     with pytest.raises(ValueError, match="slot of receiver"):
         ex._load(s, gs[1])
+
+
+def test_reload_copies_the_node_set_only_when_it_changed():
+    """A slot reloads edges every call but copies nodes / species / lists only for another chunk object or after an
+    in-place write to one of its tensors (MD keeps its chunk objects between neighbour-list rebuilds); a reload with
+    fewer edges keeps every index inside its buffer."""
+    gs = _chunks("pos")
+    n_cap, e_cap, nt_cap = chunk_graphs.capacities(max(g.n_nodes for g in gs), max(g.nE for g in gs), 24,
+                                                   e_align=64)
+    ex = chunk_graphs.ChunkGraphExec(_stub_layers(), 8, n_cap, e_cap, nt_cap, "pos", False)
+    g = gs[1]
+    s = ex.slots[1] = chunk_graphs._Slot(ex, 1)
+    ex._load(s, g)
+    s.nodes[0] = -5                               # marks the slot's copy
+    ex._load(s, g)                                # same objects, same versions: no node copy
+    assert int(s.nodes[0]) == -5
+    g.nodes[1] = g.nodes[1]                       # an in-place write bumps the tensor's version
+    ex._load(s, g)
+    assert torch.equal(s.nodes[:g.n_nodes], g.nodes)
+    # a new chunk object for the same receivers, with fewer edges: nodes reloaded, edges checked
+    h = _chunks("pos", seed=3)[1]
+    h.nE = h.nE - 5
+    h.ls, h.recv_local = h.ls[:h.nE], h.recv_local[:h.nE]
+    h.rowptr = torch.clamp(h.rowptr, max=h.nE)
+    ex._load(s, h)
+    assert torch.equal(s.nodes[:h.n_nodes], h.nodes) and bool((s.nodes[h.n_nodes:] == ex.sink).all())
+    assert torch.equal(s.ls[:h.nE], h.ls)
+    ex.check(s)
