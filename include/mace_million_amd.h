@@ -24,7 +24,7 @@ typedef void* mm_stream_t; /* hipStream_t */
 
 /* ---------------------------------------------------------------------------------------------- library */
 const char* mm_last_error(void);
-/* version of the argument conventions (4); a host binding must refuse a library of another version */
+/* version of the argument conventions (5); a host binding must refuse a library of another version */
 int mm_version(void);
 /* channel count (128), channel blocks (8, one per XCD) and channels per block (16) the kernels were built for */
 int mm_build_info(int* channels, int* channel_blocks, int* block_channels);
@@ -118,7 +118,9 @@ int mm_conv2_bwd_det(const int* rowptr, int nC, const float* e_pk, const float* 
  * form of the layer-1 convolution.  Forward: B[i][m][s * 64 + q] = sum over the receiver's edges whose sender has
  * species s of ht_q(r) Y_m (S <= 4 species, S_pad >= S species blocks, pad blocks 0) and rho[i] = sum of the edge
  * densities; the 64 -> 128-channel map, linear and skip_tp are applied by mm_linear with folded weights.
- * Backward from gB = dL/dB: part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m (one partial, for mm_edge_grad).
+ * Backward from gB = dL/dB: part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m (one partial, for mm_edge_grad).  gB is
+ * in the backward's MFMA operand order: gB[i][m][s * 64 + 16 g + k] = dL/dB[i][m][s * 64 + 4 k + g] (g < 4, k < 16),
+ * so that a lane's operands are contiguous.
  * tab: ht(r) = h3(r) f_cut(r) per knot interval, float4 (a0..a3) [M - 1][64], built by mm_spline_coeffs_flat from
  * mm_radial_mlp_f64 samples (D = 64 features, last layer = identity).  e_u: float4 (unit vector, r) per edge (as
  * written by mm_edge_geom_*); the harmonics Y(u) are evaluated in the kernels. */

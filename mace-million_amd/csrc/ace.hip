@@ -12,9 +12,9 @@
 // a wave evaluates edge eb + j of a 64-edge batch into the wave's LDS rows (16 floats per edge), from which the
 // MFMA operands are read (instead of storing and re-reading 64 B of harmonics per edge in global memory).
 //
-// Edge order of the forward: each wave lists its receiver's edges grouped by sender species (mm_ace_group), so that
-// a step of 4 edges holds one species and only that species' MFMAs issue (instead of one MFMA per species with the
-// other species' lanes zeroed).  The backward keeps the CSR order: grouping its 16-edge tiles the same way halved
+// Edge order of the forward: each wave lists its receiver's edges grouped by sender species (mm_ace_group, groups
+// padded to 8 slots), so that a pair of 4-edge steps holds one species and only that species' MFMAs issue (instead
+// of one MFMA per species with the other species' lanes zeroed).  The backward keeps the CSR order: grouping its 16-edge tiles the same way halved
 // its MFMAs for water but lengthened its per-tile latency chain (order -> edge record -> table rows) and measured
 // slower (2.04 -> 2.17 ms per launch at configuration 5).
 //
@@ -25,6 +25,8 @@
 // mm_ace1_bwd: given gB = dL/dB, per edge dL/dY_m = sum_q ht_q gB[s_e, q, m] and dL/dr = sum_m Y_m
 //   sum_q ht'_q gB[s_e, q, m]: two GEMMs per tile of 16 edges (A operand = ht or ht' of edge i at q = 4 k + g,
 //   B operand = gB), then a 16-lane sum over m.  Writes part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m.
+//   gB is read in the MFMA operand order: gB[i][m][s * 64 + 16 g + k] = dL/dB[i, s, q = 4 k + g, m] (mm_linear
+//   writes it so, through a column permutation of its weights).
 // ht is a cubic spline per knot interval: float4 (a0..a3) coef[row][64], row = table * (M - 1) + interval.
 #include "common.h"
 #include "gen/sh.h"
@@ -32,44 +34,55 @@
 #define MM_ACE_H 64
 #define MM_ACE_MAX_S 4
 #define MM_ACE_YB 64     // slots per harmonic batch (one per lane)
-#define MM_ACE_SEG 240   // edges of one species-grouped segment of a receiver
-#define MM_ACE_SLOTS 256 // slots of a segment's order list: MM_ACE_SEG edges + at most 3 pad slots per species
+#define MM_ACE_SEG 224   // edges of one species-grouped segment of a receiver
+#define MM_ACE_SLOTS 256 // slots of a segment's record list: MM_ACE_SEG edges + at most 7 pad slots per species
+#define MM_ACE_BSEG 256  // edges of one segment of a receiver in the backward (4 per lane, 16 tiles)
 
-// Species-grouped order of the segment [eb, eb + n) of a receiver's edges (n <= MM_ACE_SEG), built by one wave in
-// its LDS list `order`: order[slot] = edge offset within the segment, -1 for a pad slot.  The edges of species s
-// (the sender species, .z of the layer-1 edge record) fill the slots [first[s], first[s + 1]) in their CSR order,
-// and every group starts at a multiple of 4, so a 4-slot step of the forward holds one species: the MFMAs of the
-// other species are skipped.  first[] is wave-uniform.
+// Species-grouped records of the segment [eb, eb + n) of a receiver's edges (n <= MM_ACE_SEG), built by one wave in
+// its LDS list `rec` (one float4 per slot): rec[slot] = {t, table row, edge offset within the segment, density} for
+// an edge and {0, row 0, -1, 0} for a pad slot.  The edges of species s (the sender species, .z of the layer-1 edge
+// record) fill the slots [first[s], first[s + 1]) in their CSR order, and every group starts at a multiple of 8, so
+// a pair of 4-slot steps of the forward holds one species: the MFMAs of the other species are skipped.  The segment's
+// records are loaded once (four 16-byte loads per lane, issued together) and grouped from registers.  first[] is
+// wave-uniform.
 template <int S>
-__device__ __forceinline__ void mm_ace_group(const int* __restrict__ pk_i, int eb, int n, int lane,
-                                             int* __restrict__ order, int (&first)[S + 1]) {
+__device__ __forceinline__ void mm_ace_group(const floatx4* __restrict__ e_pk, int eb, int n, int lane,
+                                             floatx4* __restrict__ rec, int (&first)[S + 1]) {
+  static_assert(MM_ACE_SEG <= 4 * 64 && MM_ACE_SEG + 7 * MM_ACE_MAX_S <= MM_ACE_SLOTS - 4, "segment sizes");
+  floatx4 r[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) r[b] = e_pk[eb + min(64 * b + lane, n - 1)];   // (clamped: every load issued)
   int slot = 0;
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     first[s] = slot;
-    for (int b = 0; b < n; b += 64) {
-      const int j = b + lane;
-      const bool in = j < n && pk_i[4 * (eb + j) + 2] == s;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (64 * b >= n) break;   // (wave-uniform)
+      const int j = 64 * b + lane;
+      const bool in = j < n && __float_as_int(r[b].z) == s;
       const unsigned long long mask = __ballot(in);
-      if (in) order[slot + __popcll(mask & ((1ull << lane) - 1ull))] = j;
+      if (in) {
+        floatx4 q = r[b];
+        q.z = __int_as_float(j);
+        rec[slot + __popcll(mask & ((1ull << lane) - 1ull))] = q;
+      }
       slot += __popcll(mask);
     }
-    const int pad = (4 - (slot & 3)) & 3;
-    if (lane < pad) order[slot + lane] = -1;
+    const int pad = (8 - (slot & 7)) & 7;
+    if (lane < pad) rec[slot + lane] = floatx4{0.f, 0.f, __int_as_float(-1), 0.f};
     slot += pad;
   }
   first[S] = slot;
+  // the slots beyond the last group hold pad records too, so a step's rows may be loaded past the end
+  for (int j = slot + lane; j < MM_ACE_SLOTS; j += 64) rec[j] = floatx4{0.f, 0.f, __int_as_float(-1), 0.f};
   mm_wave_lds_sync();
 }
 
-// lane j: harmonics of the edge in slot sb + j (if any) into yrow[j * 16 .. + 15]
-__device__ __forceinline__ void mm_ace_y_batch(int sb, int nslot, int eb, int lane, const int* __restrict__ order,
-                                               const floatx4* __restrict__ e_u, float* __restrict__ yrow) {
+// lane j: harmonics of the edge vector u (has: the lane's slot holds an edge) into yrow[j * 16 .. + 15]
+__device__ __forceinline__ void mm_ace_y_store(const floatx4& u, bool has, int lane, float* __restrict__ yrow) {
   mm_wave_lds_sync();   // the previous batch has been read
-  const int sl = sb + lane;
-  const int oj = sl < nslot ? order[sl] : -1;
-  if (oj >= 0) {
-    const floatx4 u = e_u[eb + oj];
+  if (has) {
     float Y[16];
     mm_sh16(u.x, u.y, u.z, Y);
     floatx4* __restrict__ d = (floatx4*)(yrow + lane * 16);
@@ -81,33 +94,39 @@ __device__ __forceinline__ void mm_ace_y_batch(int sb, int nslot, int eb, int la
   mm_wave_lds_sync();
 }
 
-// (backward, CSR order) lane j: harmonics of edge eb + j (if it exists) into yrow[j * 16 .. + 15]; the edge vector of the next batch is
-// loaded one batch ahead (u_next)
-__device__ __forceinline__ void mm_ace_y_batch_csr(int eb, int e1, int lane, const floatx4* __restrict__ e_u,
-                                               floatx4& u_next, float* __restrict__ yrow) {
-  mm_wave_lds_sync();   // the previous batch has been read
-  const int ej = eb + lane;
-  if (ej < e1) {
-    const floatx4 u = u_next;
-    if (ej + MM_ACE_YB < e1) u_next = e_u[ej + MM_ACE_YB];
-    float Y[16];
-    mm_sh16(u.x, u.y, u.z, Y);
-    floatx4* __restrict__ d = (floatx4*)(yrow + lane * 16);
-    d[0] = floatx4{Y[0], Y[1], Y[2], Y[3]};
-    d[1] = floatx4{Y[4], Y[5], Y[6], Y[7]};
-    d[2] = floatx4{Y[8], Y[9], Y[10], Y[11]};
-    d[3] = floatx4{Y[12], Y[13], Y[14], Y[15]};
-  }
-  mm_wave_lds_sync();
+// edge vector of slot sl of the segment starting at eb (has = false for a pad slot or sl >= nslot, whose load reads
+// the segment's first edge: the load is unconditional)
+__device__ __forceinline__ floatx4 mm_ace_slot_u(int sl, int nslot, int eb, const floatx4* __restrict__ rec,
+                                                 const floatx4* __restrict__ e_u, bool& has) {
+  const int oj = sl < nslot ? __float_as_int(rec[sl].z) : -1;
+  has = oj >= 0;
+  return e_u[eb + max(oj, 0)];
 }
 
-// species of slot sl (wave-uniform when sl is)
-template <int S>
-__device__ __forceinline__ int mm_ace_species_of(int sl, const int (&first)[S + 1]) {
-  int sp = 0;
+// the four table rows of the forward step at slot sl (lane (i16, g): slot sl + g, features 16 mt + i16)
+__device__ __forceinline__ void mm_ace_fwd_rows(const floatx4* __restrict__ tab, const floatx4* __restrict__ rec,
+                                                int sl, int g, int i16, floatx4 (&c)[4]) {
+  const floatx4* __restrict__ tp = tab + (size_t)__float_as_int(rec[sl + g].y) * MM_ACE_H + i16;
 #pragma unroll
-  for (int s = 1; s < S; ++s) sp += sl >= first[s] ? 1 : 0;
-  return __builtin_amdgcn_readfirstlane(sp);
+  for (int mt = 0; mt < 4; ++mt) c[mt] = tp[16 * mt];
+}
+
+// one forward step: the 4 slots at sl (all of the species whose accumulators acc are) into B's accumulators
+__device__ __forceinline__ void mm_ace_fwd_step(const floatx4 (&c)[4], const floatx4* __restrict__ rec,
+                                                const float* __restrict__ yrow, int sl, int g, int i16,
+                                                floatx4 (&acc)[4], float& dsum) {
+  const floatx4 pk = rec[sl + g];
+  // a pad slot holds row 0 (finite) and density 0; its h is zeroed by a factor
+  const bool valid = __float_as_int(pk.z) >= 0;
+  const float y = valid ? yrow[((sl + g) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
+  const float t = pk.x;
+  if (i16 == 0) dsum += pk.w;
+  const float vf = valid ? 1.f : 0.f;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const float h = vf * fmaf(fmaf(fmaf(c[mt].w, t, c[mt].z), t, c[mt].y), t, c[mt].x);
+    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(h, y, acc[mt], 0, 0, 0);
+  }
 }
 
 template <int S>
@@ -117,14 +136,13 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
                                                           const floatx4* __restrict__ tab, int S_pad,
                                                           float* __restrict__ Bout, float* __restrict__ rho) {
   __shared__ float yrows[4 * MM_ACE_YB * 16];
-  __shared__ int orders[4 * MM_ACE_SLOTS];
+  __shared__ floatx4 recs[4 * MM_ACE_SLOTS];
   float* __restrict__ yrow = yrows + (threadIdx.x >> 6) * (MM_ACE_YB * 16);
-  int* __restrict__ order = orders + (threadIdx.x >> 6) * MM_ACE_SLOTS;
+  floatx4* __restrict__ rec = recs + (threadIdx.x >> 6) * MM_ACE_SLOTS;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= nC) return;   // the kernel synchronises only within a wave
   const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
   const int e0 = rowptr[i], e1 = rowptr[i + 1];
-  const int* __restrict__ pk_i = (const int*)e_pk;
   floatx4 acc[S][4];
 #pragma unroll
   for (int s = 0; s < S; ++s)
@@ -134,39 +152,39 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
   for (int eb = e0; eb < e1; eb += MM_ACE_SEG) {
     const int n = min(MM_ACE_SEG, e1 - eb);
     int first[S + 1];
-    mm_ace_group<S>(pk_i, eb, n, lane, order, first);
+    mm_ace_group<S>(e_pk, eb, n, lane, rec, first);
     const int nslot = first[S];
-    int oj_n = order[g];                                  // the step's slots are read one step ahead
-    floatx4 pk_n = oj_n >= 0 ? e_pk[eb + oj_n] : floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < nslot; k += 4) {
-      if ((k & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch(k, nslot, eb, lane, order, e_u, yrow);   // (wave-uniform)
-      const int oj = oj_n;
-      const floatx4 pk = pk_n;
-      if (k + 4 < nslot) {
-        oj_n = order[k + 4 + g];
-        pk_n = oj_n >= 0 ? e_pk[eb + oj_n] : floatx4{0.f, 0.f, 0.f, 0.f};
-      }
-      const bool valid = oj >= 0;
-      const float y = valid ? yrow[((k + g) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
-      const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + i16;
-      const float t = pk.x;
-      if (i16 == 0 && valid) dsum += pk.w;
-      // the step's four table rows are loaded together, before any use: a pad lane reads row 0 (finite) and its
-      // h is zeroed by a factor, so no load sits behind a branch on the slot's validity
-      const float vf = valid ? 1.f : 0.f;
-      floatx4 c[4];
+    // software pipeline over pairs of steps: buffer A holds the rows of the even steps, B of the odd ones, and
+    // each buffer is reloaded for the step two ahead right after its use (no register copies of loads in flight,
+    // which would make the compiler wait for them); the edge vectors of a 64-slot harmonic batch are loaded
+    // during the batch before.  A pair of steps lies in one species group, whose accumulators are known at
+    // compile time in the loop over that group.
+    floatx4 cA[4], cB[4];
+    mm_ace_fwd_rows(tab, rec, 0, g, i16, cA);
+    __builtin_amdgcn_sched_barrier(0);
+    mm_ace_fwd_rows(tab, rec, 4, g, i16, cB);
+    __builtin_amdgcn_sched_barrier(0);
+    bool u_has;
+    floatx4 u = mm_ace_slot_u(lane, nslot, eb, rec, e_u, u_has);
+    int k = 0;
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) c[mt] = tp[16 * mt];
-      __builtin_amdgcn_sched_barrier(0);
-      const int sp = mm_ace_species_of<S>(k, first);     // the step's 4 slots hold one species
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const float h = vf * fmaf(fmaf(fmaf(c[mt].w, t, c[mt].z), t, c[mt].y), t, c[mt].x);
-#pragma unroll
-        for (int s = 0; s < S; ++s)
-          if (s == sp) acc[s][mt] = __builtin_amdgcn_mfma_f32_16x16x4f32(h, y, acc[s][mt], 0, 0, 0);
+    for (int s = 0; s < S; ++s) {
+      for (; k < first[s + 1]; k += 8) {
+        if ((k & (MM_ACE_YB - 1)) == 0) {   // (wave-uniform)
+          mm_ace_y_store(u, u_has, lane, yrow);
+          u = mm_ace_slot_u(k + MM_ACE_YB + lane, nslot, eb, rec, e_u, u_has);
+        }
+        mm_ace_fwd_step(cA, rec, yrow, k, g, i16, acc[s], dsum);
+        __builtin_amdgcn_sched_barrier(0);
+        mm_ace_fwd_rows(tab, rec, min(k + 8, MM_ACE_SLOTS - 4), g, i16, cA);
+        __builtin_amdgcn_sched_barrier(0);
+        mm_ace_fwd_step(cB, rec, yrow, k + 4, g, i16, acc[s], dsum);
+        __builtin_amdgcn_sched_barrier(0);
+        mm_ace_fwd_rows(tab, rec, min(k + 12, MM_ACE_SLOTS - 4), g, i16, cB);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    mm_wave_lds_sync();   // the next segment's records replace these
   }
   // C layout: lane (j = i16, g) holds rows 4 g + v (q within the 16-block mt) of column m = j
   float* __restrict__ op = Bout + (size_t)i * 16 * S_pad * MM_ACE_H + (size_t)i16 * S_pad * MM_ACE_H + 4 * g;
@@ -182,90 +200,235 @@ __global__ void __launch_bounds__(256) mm_ace1_fwd_kernel(const int* __restrict_
   if (lane == 0) rho[i] = dsum;
 }
 
-// part rows of the 16-edge tile starting at tb: lane (i16 = m, g) holds dL/dY_m of edges tb + 4 g + v and, in every
-// lane, dL/dr of those edges
-__device__ __forceinline__ void ace_bwd_store(float* __restrict__ part, int tb, int e1, int g, int i16,
+// ------------------------------------------------------------------------------------------------ backward
+// A segment of up to MM_ACE_BSEG edges of one receiver is staged in the wave's LDS, its edges listed by sender
+// species (slots [first[s], first[s + 1]) hold species s, CSR order within a species, no padding between groups):
+// rec[slot] = {t, table row, edge offset in the segment, 0} and uv[slot] = the edge vector; slots beyond the segment
+// hold pad records (row 0, edge -1).  A tile of 16 slots holds one species except at a group boundary, so most
+// tiles issue one species' MFMAs instead of one set per species with the other species' lanes zeroed.
+//
+// Table rows are loaded coalesced: in half kh of a tile, load j (< 8) of a lane reads feature q = 32 kh + (lane & 31)
+// of slot 2 j + (lane >> 5), so each half-wave reads 512 contiguous bytes of one row (in the MFMA layout, lane
+// (i, g) would need edge i's row and the 16 lanes of a row group would read 16 different rows, which the texture
+// path serves one lane per clock).  The cubic is evaluated in that layout and h, h' are passed to the MFMA layout
+// through the wave's LDS (hT[edge i][g][k], 2 KiB each for one half).
+template <int S>
+__device__ __forceinline__ void ace_bwd_stage(const floatx4* __restrict__ e_pk, const floatx4* __restrict__ e_u,
+                                              int sb, int n, int lane, floatx4* __restrict__ rec,
+                                              floatx4* __restrict__ uv, int (&first)[S + 1]) {
+  floatx4 r[4], u[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {   // (clamped: every load issued)
+    const int j = sb + min(64 * b + lane, n - 1);
+    r[b] = e_pk[j];
+    u[b] = e_u[j];
+  }
+  mm_wave_lds_sync();   // the previous segment has been read
+  int slot = 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    first[s] = slot;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (64 * b >= n) break;   // (wave-uniform)
+      const int j = 64 * b + lane;
+      const bool in = j < n && __float_as_int(r[b].z) == s;
+      const unsigned long long mask = __ballot(in);
+      if (in) {
+        const int sl = slot + __popcll(mask & ((1ull << lane) - 1ull));
+        rec[sl] = floatx4{r[b].x, r[b].y, __int_as_float(j), 0.f};
+        uv[sl] = u[b];
+      }
+      slot += __popcll(mask);
+    }
+  }
+  first[S] = slot;
+  for (int j = slot + lane; j < MM_ACE_BSEG; j += 64) {
+    rec[j] = floatx4{0.f, 0.f, __int_as_float(-1), 0.f};
+    uv[j] = floatx4{0.f, 0.f, 1.f, 0.f};
+  }
+  mm_wave_lds_sync();
+}
+
+// species of slot sl (wave-uniform when sl is)
+template <int S>
+__device__ __forceinline__ int ace_species_of(int sl, const int (&first)[S + 1]) {
+  int sp = 0;
+#pragma unroll
+  for (int s = 1; s < S; ++s) sp += sl >= first[s] ? 1 : 0;
+  return sp;
+}
+
+// coalesced rows of half kh of the tile at slot tb (see above); tb <= MM_ACE_BSEG - 16
+__device__ __forceinline__ void ace_bwd_load_half(const floatx4* __restrict__ tab, const floatx4* __restrict__ rec,
+                                                  int tb, int kh, int lane, floatx4 (&c)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = __float_as_int(rec[tb + 2 * j + (lane >> 5)].y);
+    c[j] = tab[(size_t)row * MM_ACE_H + 32 * kh + (lane & 31)];
+  }
+}
+
+// h and h' of half kh from its coalesced rows, into hT / hpT[edge i][g][k] (feature 32 kh + 4 k + g), then read back
+// in the MFMA layout: lane (i16, g) gets h[k] = h(edge i16, feature 32 kh + 4 k + g), k < 8
+__device__ __forceinline__ void ace_bwd_h_half(const floatx4 (&c)[8], const floatx4* __restrict__ rec, int tb,
+                                               int lane, int i16, int g, float* __restrict__ hT,
+                                               float* __restrict__ hpT, float (&h)[8], float (&hp)[8]) {
+  const int qh = lane & 31;
+  const int wofs = (lane >> 5) * 32 + (qh & 3) * 8 + (qh >> 2);   // (edge 2 j + (lane >> 5), g = qh & 3, k = qh >> 2)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float t = rec[tb + 2 * j + (lane >> 5)].x;
+    hT[64 * j + wofs] = fmaf(fmaf(fmaf(c[j].w, t, c[j].z), t, c[j].y), t, c[j].x);
+    hpT[64 * j + wofs] = fmaf(fmaf(3.f * c[j].w, t, 2.f * c[j].z), t, c[j].y);
+  }
+  mm_wave_lds_sync();
+  const floatx4* __restrict__ hr = (const floatx4*)(hT + (i16 * 4 + g) * 8);
+  const floatx4* __restrict__ hpr = (const floatx4*)(hpT + (i16 * 4 + g) * 8);
+  const floatx4 h0 = hr[0], h1 = hr[1], p0 = hpr[0], p1 = hpr[1];
+  h[0] = h0.x; h[1] = h0.y; h[2] = h0.z; h[3] = h0.w; h[4] = h1.x; h[5] = h1.y; h[6] = h1.z; h[7] = h1.w;
+  hp[0] = p0.x; hp[1] = p0.y; hp[2] = p0.z; hp[3] = p0.w; hp[4] = p1.x; hp[5] = p1.y; hp[6] = p1.z; hp[7] = p1.w;
+  mm_wave_lds_sync();   // read before the next half overwrites hT
+}
+
+// the MFMAs of half kh: K-steps 8 kh + k of dY (A operand h) and dYp (A operand h'), one set per species present in
+// the tile (s_lo .. s_hi, wave-uniform), the lanes of other species (and pad slots, se = -1) zeroed
+template <int S>
+__device__ __forceinline__ void ace_bwd_mfma_half(const float (&h)[8], const float (&hp)[8], int se, int s_lo,
+                                                  int s_hi, const float (&gb)[S][16], int kh, floatx4& dY,
+                                                  floatx4& dYp) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (s < s_lo || s > s_hi) continue;   // (wave-uniform)
+    const float fs = se == s ? 1.f : 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      dY = __builtin_amdgcn_mfma_f32_16x16x4f32(h[k] * fs, gb[s][8 * kh + k], dY, 0, 0, 0);
+      dYp = __builtin_amdgcn_mfma_f32_16x16x4f32(hp[k] * fs, gb[s][8 * kh + k], dYp, 0, 0, 0);
+    }
+  }
+}
+
+// part rows of a tile: lane (i16 = m, g) holds dL/dY_m of the slots 4 g + v, whose edges are ev[v] (-1: none), and,
+// in every lane, dL/dr of those edges
+__device__ __forceinline__ void ace_bwd_store(float* __restrict__ part, const int (&ev)[4], int i16,
                                               const floatx4& dY, const float (&gr)[4]) {
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
-    const int ev = tb + 4 * g + v;
-    if (ev < e1) {
-      float* __restrict__ pp = part + (size_t)ev * 17;
+    if (ev[v] >= 0) {
+      float* __restrict__ pp = part + (size_t)ev[v] * 17;
       pp[1 + i16] = dY[v];
       if (i16 == 0) pp[0] = gr[v];
     }
   }
 }
 
+// One wave per receiver, tiles of 16 slots of its species-ordered segments.  The loop is software-pipelined by
+// halves of a tile: the next tile's first-half rows are loaded once this tile's first half has been evaluated, its
+// second-half rows once this tile's second half has been, so half a tile of rows (8 loads per lane) is in flight
+// at any time, and a buffer is reloaded only after its last use (no register copies of loads in flight, which would
+// make the compiler wait for them).  The part rows of a tile are stored during the next tile, before its row loads,
+// so that waiting for rows never waits for fresh stores (the wait counter counts both, in order).
 template <int S>
-__global__ void __launch_bounds__(256) mm_ace1_bwd_kernel(const int* __restrict__ rowptr, int nC,
-                                                          const floatx4* __restrict__ e_pk,
-                                                          const floatx4* __restrict__ e_u,
-                                                          const floatx4* __restrict__ tab, int S_pad,
-                                                          const float* __restrict__ gB, float inv_h,
-                                                          float* __restrict__ part) {
-  __shared__ float yrows[4 * MM_ACE_YB * 16];
-  float* __restrict__ yrow = yrows + (threadIdx.x >> 6) * (MM_ACE_YB * 16);
-  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(S <= 2 ? 3 : 2)))
+mm_ace1_bwd_kernel(const int* __restrict__ rowptr, int nC, const floatx4* __restrict__ e_pk,
+                   const floatx4* __restrict__ e_u, const floatx4* __restrict__ tab, int S_pad,
+                   const float* __restrict__ gB, float inv_h, float* __restrict__ part) {
+  __shared__ floatx4 recs[4 * MM_ACE_BSEG];
+  __shared__ floatx4 uvs[4 * MM_ACE_BSEG];
+  __shared__ float yts[4 * 16 * 16];
+  __shared__ float hts[4 * 2 * 16 * 32];
+  const int w = threadIdx.x >> 6;
+  floatx4* __restrict__ rec = recs + w * MM_ACE_BSEG;
+  floatx4* __restrict__ uv = uvs + w * MM_ACE_BSEG;
+  float* __restrict__ yt = yts + w * 256;
+  float* __restrict__ hT = hts + w * 1024;
+  float* __restrict__ hpT = hT + 512;
+  const int i = blockIdx.x * 4 + w;
   if (i >= nC) return;
   const int lane = threadIdx.x & 63, i16 = lane & 15, g = lane >> 4;
   const int e0 = rowptr[i], e1 = rowptr[i + 1];
-  // B operand of step k (4 q x 16 m): lane (j = i16, g) holds gB[i][m = j][s * 64 + 4 k + g]
+  if (e0 >= e1) return;
+  int n = min(MM_ACE_BSEG, e1 - e0);
+  int first[S + 1];
+  ace_bwd_stage<S>(e_pk, e_u, e0, n, lane, rec, uv, first);
+  // B operand of step k (4 q x 16 m): lane (j = i16, g) holds dL/dB[i, s, q = 4 k + g, m = j].  gB stores it in
+  // this operand order, gB[i][m][s * 64 + 16 g + k], so a lane's 16 values of one species are 64 contiguous bytes
+  // (four 16-byte loads per species instead of sixteen 4-byte loads).
   float gb[S][16];
-  const float* __restrict__ gp = gB + (size_t)i * 16 * S_pad * MM_ACE_H + (size_t)i16 * S_pad * MM_ACE_H + g;
+  const floatx4* __restrict__ gp =
+      (const floatx4*)(gB + (size_t)i * 16 * S_pad * MM_ACE_H + (size_t)i16 * S_pad * MM_ACE_H + 16 * g);
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
-    for (int k = 0; k < 16; ++k) gb[s][k] = gp[s * MM_ACE_H + 4 * k];
-  // the packed record of the next tile is loaded one tile ahead; the tile's harmonics before its MFMAs
-  floatx4 pk_n = e0 + i16 < e1 ? e_pk[e0 + i16] : floatx4{0.f, 0.f, 0.f, 0.f};
-  floatx4 u_next = e0 + lane < e1 ? e_u[e0 + lane] : floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 4; ++kk) {
+      const floatx4 wv = gp[s * (MM_ACE_H / 4) + kk];
+      gb[s][4 * kk] = wv.x;
+      gb[s][4 * kk + 1] = wv.y;
+      gb[s][4 * kk + 2] = wv.z;
+      gb[s][4 * kk + 3] = wv.w;
+    }
   floatx4 sdY = {0.f, 0.f, 0.f, 0.f};
   float sgr[4] = {0.f, 0.f, 0.f, 0.f};
-  int stb = -1;
-  for (int tb = e0; tb < e1; tb += 16) {
-    if (((tb - e0) & (MM_ACE_YB - 1)) == 0) mm_ace_y_batch_csr(tb, e1, lane, e_u, u_next, yrow);   // (wave-uniform)
-    const int e = tb + i16;          // A-operand row: edge i16 of the tile
-    const bool valid = e < e1;
-    const floatx4 pk = pk_n;
-    if (e + 16 < e1) pk_n = e_pk[e + 16];
-    float yv[4];
+  int sev[4] = {-1, -1, -1, -1};   // edges of the tile whose part rows are pending (-1: none)
+  for (int sb = e0; sb < e1; sb += MM_ACE_BSEG) {
+    if (sb != e0) {
+      // the pending rows name edges of the previous segment, whose records the stage replaces: store them first
+      ace_bwd_store(part, sev, i16, sdY, sgr);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int ev = tb + 4 * g + v;
-      yv[v] = ev < e1 ? yrow[((ev - e0) & (MM_ACE_YB - 1)) * 16 + i16] : 0.f;
+      for (int v = 0; v < 4; ++v) sev[v] = -1;
+      n = min(MM_ACE_BSEG, e1 - sb);
+      ace_bwd_stage<S>(e_pk, e_u, sb, n, lane, rec, uv, first);
     }
-    const int se = valid ? __float_as_int(pk.z) : -1;
-    const floatx4* __restrict__ tp = tab + (size_t)(valid ? __float_as_int(pk.y) : 0) * MM_ACE_H + g;
-    const float t = pk.x;
-    // the tile's 16 table rows are loaded together, before any use (one memory latency per tile); a pad lane reads
-    // row 0 (finite) and its A operands are zeroed by the species factors
-    floatx4 c[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) c[k] = tp[4 * k];
-    if (stb >= 0) ace_bwd_store(part, stb, e1, g, i16, sdY, sgr);   // the previous tile's results
+    floatx4 cA[8], cB[8];
+    __builtin_amdgcn_sched_barrier(0);   // the loop's wait counts assume the first half issued first
+    ace_bwd_load_half(tab, rec, 0, 0, lane, cA);
     __builtin_amdgcn_sched_barrier(0);
-    float fs[S];   // 1 for the species of this lane's edge, else 0
-#pragma unroll
-    for (int s = 0; s < S; ++s) fs[s] = se == s ? 1.f : 0.f;
-    floatx4 dY = {0.f, 0.f, 0.f, 0.f}, dYp = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float h = fmaf(fmaf(fmaf(c[k].w, t, c[k].z), t, c[k].y), t, c[k].x);
-      const float hp = fmaf(fmaf(3.f * c[k].w, t, 2.f * c[k].z), t, c[k].y);
-#pragma unroll
-      for (int s = 0; s < S; ++s) {
-        dY = __builtin_amdgcn_mfma_f32_16x16x4f32(h * fs[s], gb[s][k], dY, 0, 0, 0);
-        dYp = __builtin_amdgcn_mfma_f32_16x16x4f32(hp * fs[s], gb[s][k], dYp, 0, 0, 0);
+    ace_bwd_load_half(tab, rec, 0, 1, lane, cB);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int tb = 0; tb < n; tb += 16) {
+      const int tbn = min(tb + 16, MM_ACE_BSEG - 16);   // next tile's rows (after the last: pad rows, unused)
+      const int s_lo = ace_species_of<S>(tb, first), s_hi = ace_species_of<S>(min(tb + 15, n - 1), first);
+      const int se = tb + i16 < n ? ace_species_of<S>(tb + i16, first) : -1;
+      // harmonics of the tile's 16 edges: lane j < 16 evaluates slot tb + j into yt[j][m]
+      {
+        const floatx4 uu = uv[tb + i16];
+        float Y[16];
+        mm_sh16(uu.x, uu.y, uu.z, Y);
+        if (lane < 16) {
+          floatx4* __restrict__ d = (floatx4*)(yt + lane * 16);
+          d[0] = floatx4{Y[0], Y[1], Y[2], Y[3]};
+          d[1] = floatx4{Y[4], Y[5], Y[6], Y[7]};
+          d[2] = floatx4{Y[8], Y[9], Y[10], Y[11]};
+          d[3] = floatx4{Y[12], Y[13], Y[14], Y[15]};
+        }
       }
-    }
-    // C layout: lane (j = i16 = m, g) holds edges tb + 4 g + v of column m
+      floatx4 dY = {0.f, 0.f, 0.f, 0.f}, dYp = {0.f, 0.f, 0.f, 0.f};
+      float h[8], hp[8];
+      ace_bwd_h_half(cA, rec, tb, lane, i16, g, hT, hpT, h, hp);
+      __builtin_amdgcn_sched_barrier(0);
+      ace_bwd_store(part, sev, i16, sdY, sgr);   // the previous tile's results
+      ace_bwd_load_half(tab, rec, tbn, 0, lane, cA);
+      __builtin_amdgcn_sched_barrier(0);
+      ace_bwd_mfma_half<S>(h, hp, se, s_lo, s_hi, gb, 0, dY, dYp);
+      ace_bwd_h_half(cB, rec, tb, lane, i16, g, hT, hpT, h, hp);
+      __builtin_amdgcn_sched_barrier(0);
+      ace_bwd_load_half(tab, rec, tbn, 1, lane, cB);
+      __builtin_amdgcn_sched_barrier(0);
+      ace_bwd_mfma_half<S>(h, hp, se, s_lo, s_hi, gb, 1, dY, dYp);
+      // C layout: lane (j = i16 = m, g) holds slots tb + 4 g + v of column m
 #pragma unroll
-    for (int v = 0; v < 4; ++v) sgr[v] = mm_row_sum16(dYp[v] * yv[v]) * inv_h;
-    sdY = dY;
-    stb = tb;
+      for (int v = 0; v < 4; ++v) {
+        const int sl = tb + 4 * g + v;
+        const int ej = __float_as_int(rec[sl].z);
+        const float yv = ej >= 0 ? yt[(4 * g + v) * 16 + i16] : 0.f;
+        sgr[v] = mm_row_sum16(dYp[v] * yv) * inv_h;
+        sev[v] = ej >= 0 ? sb + ej : -1;
+      }
+      sdY = dY;
+    }
   }
-  if (stb >= 0) ace_bwd_store(part, stb, e1, g, i16, sdY, sgr);
+  ace_bwd_store(part, sev, i16, sdY, sgr);
 }
 
 template <int S>

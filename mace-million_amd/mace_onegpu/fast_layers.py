@@ -32,6 +32,14 @@ ACE_H = 64                      # hidden features of the layer-1 ACE kernels (cs
 ACE_MAX_S = 4                   # species per system of the layer-1 ACE kernels
 
 
+def ace_gb_order(n_species):
+    """Column order of dL/dB that mm_ace1_bwd reads (its MFMA operand order): position s * 64 + 16 g + k holds
+    feature q = 4 k + g of species block s (g < 4, k < 16), so that each lane's 16 operands are contiguous."""
+    p = torch.arange(n_species * ACE_H)
+    s, g, k = p // ACE_H, (p % ACE_H) // 16, p % 16
+    return s * ACE_H + 4 * k + g
+
+
 def split3_bf16(W):
     """fp32 W -> (W0, W1, W2) bf16 with W0 = bf16(W), W1 = bf16(W - W0), W2 = bf16(W - W0 - W1) (round to nearest
     even; the differences are exact in fp32): |W - W0 - W1 - W2| <= 2^-27 |W|."""
@@ -287,7 +295,7 @@ class FastLayers:
                 for j in range(nJ):
                     blk = full[j * 128:(j + 1) * 128]
                     Gs.append(blk)
-                    GTs.append(blk.T)
+                    GTs.append(blk.T[:, ace_gb_order(2)])   # gB columns in mm_ace1_bwd's operand order
         self.W_ace = torch.cat([mfma_block(m.to(torch.float32)) for m in Gs]).to(dev)
         self.W_aceT = torch.cat([mfma_block(m.to(torch.float32)) for m in GTs]).to(dev)
         Kp = self.S_pad * H

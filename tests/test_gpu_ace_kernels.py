@@ -5,8 +5,9 @@ Semantics checked (the density-projection form of layer 1, reference ace_layer1.
     h_q(e)        = a0 + t (a1 + t (a2 + t a3)),  (a0..a3) = table row of edge e, feature q (64 features)
     B[i, m, s, q] = sum_{e: recv(e) = i, species(e) = s} h_q(e) Y_m(u_e),    rho[i] = sum_e density(e)
     part[e, 1+m]  = sum_q h_q(e) gB[i, m, s_e, q],   part[e, 0] = inv_h sum_m Y_m(u_e) sum_q h'_q(e) gB[i, m, s_e, q]
-Receiver degrees sit at and around the kernels' 64-slot harmonic batches, 16-slot backward tiles and 240-edge
-species-grouped segments.
+(the backward takes gB with its columns in the kernel's MFMA operand order, fast_layers.ace_gb_order)
+Receiver degrees sit at and around the kernels' 64-slot harmonic batches, 16-edge backward tiles (8-slot forward step
+pairs), 224-edge species-grouped forward segments and 256-edge backward segments; every special degree occurs.
 """
 import numpy as np
 import pytest
@@ -19,7 +20,9 @@ H = 64
 
 def _case(seed, nC, S, S_pad, NR=11):
     rng = np.random.default_rng(seed)
-    deg = rng.choice([0, 1, 3, 15, 16, 17, 63, 64, 65, 80, 128, 129, 239, 240, 241, 300, 481], nC)
+    special = [0, 1, 3, 7, 8, 9, 15, 16, 17, 63, 64, 65, 80, 128, 129, 223, 224, 225, 255, 256, 257, 300, 449, 513]
+    deg = np.concatenate([special, rng.choice(special, nC - len(special))])
+    rng.shuffle(deg)
     rowptr = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
     E = int(rowptr[-1])
     u = rng.normal(size=(E, 3))
@@ -73,7 +76,8 @@ def test_ace_kernels_against_fp64(S, S_pad):
     eu[:, 3] = torch.tensor(cs["r"], **f32)
     rowptr = torch.tensor(cs["rowptr"], dtype=torch.int32, device=dev)
     tab = torch.tensor(cs["tab"], **f32).contiguous()
-    gB = torch.tensor(cs["gB"], **f32).contiguous()
+    from mace_onegpu.fast_layers import ace_gb_order
+    gB = torch.tensor(cs["gB"], **f32).reshape(nC, 16, S_pad * H)[:, :, ace_gb_order(S_pad)].contiguous()
     B = torch.full((nC, 16 * S_pad * H), float("nan"), **f32)
     rho = torch.full((nC,), float("nan"), **f32)
     part = torch.full((E * 17 + 9,), float("nan"), **f32)

@@ -38,3 +38,17 @@ def test_block_order_is_the_b_operand_layout():
     # the order is a permutation: the plane sums are the matrix sums
     for p in range(3):
         assert torch.isclose(blk[p * 16384:(p + 1) * 16384].double().sum(), planes[p].double().sum(), rtol=1e-12)
+
+
+def test_ace_gb_order_is_the_backward_operand_order():
+    """mm_ace1_bwd's lane (m, g) reads 16 contiguous values per species block s, the operands of K-steps k = 0..15:
+    position s * 64 + 16 g + k of its gB row must hold feature q = 4 k + g (every feature once per block)."""
+    from mace_onegpu.fast_layers import ace_gb_order
+    for S_pad in (2, 4):
+        order = ace_gb_order(S_pad)
+        assert sorted(order.tolist()) == list(range(S_pad * 64))
+        row = torch.arange(S_pad * 64)[order]          # what a gB row in operand order holds at each position
+        for s in range(S_pad):
+            for g in range(4):
+                lane = row[s * 64 + 16 * g:s * 64 + 16 * g + 16]
+                assert lane.tolist() == [s * 64 + 4 * k + g for k in range(16)]
