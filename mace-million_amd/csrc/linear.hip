@@ -23,7 +23,8 @@
 // Weight blocks: plane p of block b at bf16 offset (3 b + p) 16384; element W[k][n], k = 32 t + 8 g + u,
 // n = 16 nt + i, at (((t * 8 + nt) * 4 + g) * 16 + i) * 8 + u, so that lane (i, g) reads its 8 k-values of step t
 // and tile nt as one 16-byte LDS read, the 16 lanes of a group reading 256 consecutive bytes (no bank conflicts);
-// the A operand of lane (row, g) is in[row][32 t + 8 g .. + 7].
+// the A operand of lane (row, g) is in[row][32 t + 8 g .. + 7], loaded coalesced and passed through 2.5 KiB of
+// LDS rows per wave (mm_lin_load_a, mm_lin_stage_a); a row past the last one reads logical row 0 and is not stored.
 #include "common.h"
 
 #include <algorithm>
@@ -32,6 +33,7 @@
 #define MM_LIN_MAX_SRC 3
 #define MM_LIN_NW 16
 #define MM_LIN_BLOCK_ROWS (16 * MM_LIN_NW)
+#define MM_LIN_AS 40   // LDS row stride (floats) of a wave's A staging rows
 // a launch keeps at least this many workgroups (4 per CU) when it groups row blocks per workgroup
 #define MM_LIN_MIN_WG 1024
 
@@ -78,15 +80,34 @@ __device__ __forceinline__ void mm_lin_rows(const MMLinArgs& args, const int* li
   rw.in_row = args.in_rows ? (long)args.in_rows[rid] : (long)rid;
 }
 
-// A operands of one source: lane (i, g) holds in[row i][32 t + 8 g .. + 7] in a[2 t], a[2 t + 1] (t = 0..3)
-__device__ __forceinline__ void mm_lin_load_a(const MMLinArgs& args, const MMLinRows& rw, int in_off, int g,
+// Input rows of one source, loaded coalesced: lane L reads rows L >> 3 and 8 + (L >> 3) of the wave's 16, floats
+// 32 t + 4 (L & 7) .. + 3 of the source chunk, into a[2 t] and a[2 t + 1] (t = 0..3): 8 lanes read 128 contiguous
+// bytes of a row.  (In the MFMA operand layout the 16 lanes of a row group would read 16 different rows, which the
+// texture path serves one lane per clock.)  mm_lin_stage_a passes step t through the wave's LDS rows into the
+// operand layout.
+__device__ __forceinline__ void mm_lin_load_a(const MMLinArgs& args, const MMLinRows& rw, int in_off, int lane,
                                               floatx4 (&a)[8]) {
-  const float* __restrict__ ap = args.in + rw.in_row * args.in_stride + in_off + 8 * g;
+  const long r0 = __shfl(rw.in_row, lane >> 3), r1 = __shfl(rw.in_row, 8 + (lane >> 3));
+  const float* __restrict__ p0 = args.in + r0 * args.in_stride + in_off + 4 * (lane & 7);
+  const float* __restrict__ p1 = args.in + r1 * args.in_stride + in_off + 4 * (lane & 7);
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    a[2 * t] = rw.valid ? *(const floatx4*)(ap + 32 * t) : floatx4{0.f, 0.f, 0.f, 0.f};
-    a[2 * t + 1] = rw.valid ? *(const floatx4*)(ap + 32 * t + 4) : floatx4{0.f, 0.f, 0.f, 0.f};
+    a[2 * t] = *(const floatx4*)(p0 + 32 * t);
+    a[2 * t + 1] = *(const floatx4*)(p1 + 32 * t);
   }
+}
+
+// A operand of step t: lane (i, g) gets in[row i][32 t + 8 g .. + 7], through the wave's LDS rows (row stride
+// MM_LIN_AS floats: the 16-byte reads of the 16 rows fall in different banks)
+__device__ __forceinline__ floatx8 mm_lin_stage_a(const floatx4 (&a)[8], int t, int lane, int i, int g,
+                                                  float* __restrict__ as) {
+  mm_wave_lds_sync();   // the previous step's reads are done
+  *(floatx4*)(as + (lane >> 3) * MM_LIN_AS + 4 * (lane & 7)) = a[2 * t];
+  *(floatx4*)(as + (8 + (lane >> 3)) * MM_LIN_AS + 4 * (lane & 7)) = a[2 * t + 1];
+  mm_wave_lds_sync();
+  const floatx4 xa = *(const floatx4*)(as + i * MM_LIN_AS + 8 * g);
+  const floatx4 xb = *(const floatx4*)(as + i * MM_LIN_AS + 8 * g + 4);
+  return floatx8{xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 }
 
 // x = x0 + x1 + x2 (bf16, round to nearest even; both differences are exact in fp32)
@@ -102,6 +123,7 @@ __device__ __forceinline__ void mm_split3_bf16(const floatx8& x, bf16x8& x0, bf1
 // is staged in LDS once for all of them.
 __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs args, int n_blk) {
   __shared__ uint4 Wl[3 * 2048];
+  __shared__ float As_all[MM_LIN_NW * 16 * MM_LIN_AS];   // per wave: 16 rows of one K-step
   const MMLinComp& cp = args.comp[blockIdx.x];   // kernel-argument memory, read with uniform indices
   const int grp = blockIdx.z;
   const int nrows = args.list_count ? min(args.list_count[grp], args.n_rows) : args.n_rows;
@@ -110,6 +132,7 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
   const int blk1 = min(blk0 + n_blk, (nrows + MM_LIN_BLOCK_ROWS - 1) / MM_LIN_BLOCK_ROWS);
   const int* __restrict__ list = args.list ? args.list + (size_t)grp * args.list_stride : nullptr;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  float* __restrict__ as = As_all + wave * 16 * MM_LIN_AS;
   const int n_src = cp.n_src;
   const bool restage = n_src > 1;
   MMLinRows rw;
@@ -121,7 +144,7 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
     for (int nt = 0; nt < 8; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int q = 0; q < n_src; ++q) {
       floatx4 a[8];
-      mm_lin_load_a(args, rw, cp.in_off[q], g, a);
+      mm_lin_load_a(args, rw, cp.in_off[q], lane, a);
       if (restage || blk == blk0) {
         const uint4* __restrict__ Wg = args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 6144;
         __syncthreads();
@@ -130,8 +153,7 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const floatx8 x = {a[2 * t].x, a[2 * t].y, a[2 * t].z, a[2 * t].w,
-                           a[2 * t + 1].x, a[2 * t + 1].y, a[2 * t + 1].z, a[2 * t + 1].w};
+        const floatx8 x = mm_lin_stage_a(a, t, lane, i, g, as);
         bf16x8 a0, a1, a2;
         mm_split3_bf16(x, a0, a1, a2);
 #pragma unroll
