@@ -674,6 +674,59 @@ def free_gpu():
     torch.cuda.reset_peak_memory_stats()
 
 
+def symc_gemm_probe():
+    """The layer-1 symmetric contraction as the kernel runs it against the dense-monomial form a matrix-core version
+    would need, on 131,072 nodes of one species.  The contraction is channelwise: out[n, M, c] = sum over the 968
+    monomials (degree 1..3) of x[n, :, c] times a coefficient that depends on (monomial, M, species, c), so it is a
+    batched GEMM over the 128 channels, [nodes, 968] x [968, 4 outputs] (4 padded to the 16 columns of an MFMA tile).
+    Timed: mm_symc1_fwd as built; forming the monomials (torch elementwise ops on a slice of 8,192 nodes, scaled);
+    the batched fp32 GEMM of that slice in hipBLASLt (torch.bmm), scaled, with 4 and 16 output columns."""
+    import torch
+
+    from mace_onegpu import model as mm
+    from mace_onegpu._lib import K, stream
+    from mace_onegpu.fast_layers import FastLayers
+    C, n, nb = 128, 131072, 8192
+    fl = FastLayers(mm.MaceModel(seed=0), [0, 7], device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(n, 16 * C, device="cuda", generator=g)
+    spec = torch.zeros(n, dtype=torch.int32, device="cuda")
+    out = torch.empty(n, 4 * C, device="cuda")
+
+    def timed(fn, k=10):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(k):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / k
+
+    t_kernel = timed(lambda: K.mm_symc1_fwd(n, x, 16 * C, spec, fl.Wsc1, out, 4 * C, stream()))
+    xs = x[:nb].view(nb, 16, C).permute(2, 0, 1).contiguous()            # [C, nb, 16]
+    i2 = torch.tensor([(i, j) for i in range(16) for j in range(i, 16)], device="cuda")
+    i3 = torch.tensor([(i, j, k) for i in range(16) for j in range(i, 16) for k in range(j, 16)], device="cuda")
+    form = lambda: torch.cat([xs, xs[..., i2[:, 0]] * xs[..., i2[:, 1]],
+                              xs[..., i3[:, 0]] * xs[..., i3[:, 1]] * xs[..., i3[:, 2]]], -1)
+    A = form()                                                             # [C, nb, 968]
+    t_form = timed(form)
+    res = {}
+    for nout in (4, 16):
+        B = torch.randn(C, A.shape[-1], nout, device="cuda", generator=g)
+        t = timed(lambda: torch.bmm(A, B))
+        res[nout] = (t, 2.0 * C * nb * A.shape[-1] * nout / (t * 1e-3) / 1e12)
+    scale = n / nb
+    print(json.dumps({"probe": "symmetric contraction, layer 1, 131072 nodes x 128 channels, one species",
+                      "monomials": int(A.shape[-1]), "mm_symc1_fwd_ms": round(t_kernel, 4),
+                      "form_monomials_ms_scaled": round(t_form * scale, 3),
+                      "bmm_fp32_4col_ms_scaled": round(res[4][0] * scale, 3), "bmm_fp32_4col_TFLOPs": round(res[4][1], 2),
+                      "bmm_fp32_16col_ms_scaled": round(res[16][0] * scale, 3),
+                      "bmm_fp32_16col_TFLOPs": round(res[16][1], 2)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -690,8 +743,13 @@ def main():
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed steps, run a plain elementwise kernel over this many MiB (reads and "
                          "writes a buffer of known size: calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--symc-gemm-probe", action="store_true",
+                    help="time the layer-1 symmetric contraction against its dense-monomial GEMM form and exit")
     a = ap.parse_args()
     a.cpu_from = None
+    if a.symc_gemm_probe:
+        symc_gemm_probe()
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         exit_multi_gpu()
     only = a.config is not None
