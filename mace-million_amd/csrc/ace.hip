@@ -8,15 +8,14 @@
 // (the reference's ace_layer1.py:1-104 states the identity).  The per-edge work is the outer product ht x Y;
 // the 64 -> 128-channel maps (and the following linear / skip_tp) become one GEMM per atom (mm_linear).
 //
-// Harmonics: both kernels read the 16-byte edge vector (unit vector, r) and evaluate Y(u) once per edge: lane j of
-// a wave evaluates edge eb + j of a 64-edge batch into the wave's LDS rows (16 floats per edge), from which the
-// MFMA operands are read (instead of storing and re-reading 64 B of harmonics per edge in global memory).
+// Harmonics: both kernels read the 16-byte edge vector (unit vector, r) and evaluate Y(u) once per edge into the
+// wave's LDS rows (the forward for 64-slot batches, the backward for each 16-edge tile), from which the MFMA
+// operands are read (instead of storing and re-reading 64 B of harmonics per edge in global memory).
 //
-// Edge order of the forward: each wave lists its receiver's edges grouped by sender species (mm_ace_group, groups
-// padded to 8 slots), so that a pair of 4-edge steps holds one species and only that species' MFMAs issue (instead
-// of one MFMA per species with the other species' lanes zeroed).  The backward keeps the CSR order: grouping its 16-edge tiles the same way halved
-// its MFMAs for water but lengthened its per-tile latency chain (order -> edge record -> table rows) and measured
-// slower (2.04 -> 2.17 ms per launch at configuration 5).
+// Edge order: each wave lists its receiver's edges grouped by sender species in LDS.  In the forward the groups are
+// padded to 8 slots, so that a pair of 4-edge steps holds one species and only that species' MFMAs issue (instead
+// of one MFMA per species with the other species' lanes zeroed).  In the backward the groups are not padded: a
+// 16-edge tile holds one species except at a group boundary, where it issues one MFMA set per species present.
 //
 // mm_ace1_fwd: one wave per receiver; B_i accumulated with v_mfma_f32_16x16x4f32 taking 4 edges per step:
 //   A operand (16 q x 4 edges) = ht, lane (i, g) -> q = 16 mt + i of edge g; B operand (4 edges x 16 m) = Y.
@@ -24,7 +23,8 @@
 //   densities.
 // mm_ace1_bwd: given gB = dL/dB, per edge dL/dY_m = sum_q ht_q gB[s_e, q, m] and dL/dr = sum_m Y_m
 //   sum_q ht'_q gB[s_e, q, m]: two GEMMs per tile of 16 edges (A operand = ht or ht' of edge i at q = 4 k + g,
-//   B operand = gB), then a 16-lane sum over m.  Writes part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m.
+//   B operand = gB), then a 16-lane sum over m.  Writes part[e][0] = dL/dr, part[e][1 + m] = dL/dY_m.  The table
+//   rows are loaded coalesced and ht, ht' reach the MFMA layout through LDS (see the backward section below).
 //   gB is read in the MFMA operand order: gB[i][m][s * 64 + 16 g + k] = dL/dB[i, s, q = 4 k + g, m] (mm_linear
 //   writes it so, through a column permutation of its weights).
 // ht is a cubic spline per knot interval: float4 (a0..a3) coef[row][64], row = table * (M - 1) + interval.
