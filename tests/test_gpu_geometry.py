@@ -80,8 +80,10 @@ def test_edge_geometry_against_fp64(x_from_spec):
     close("unit vector", e_u[:, :3], v / rr[:, None], 3e-7)
     close("r", e_u[:, 3], rr, 2e-7 * r_max)
     close("t", e_pk[:, 0].double(), x - kk, 1e-4)
-    close("density", e_pk[:, 3].double(), d, 3e-6 * float(d.abs().max()) + 1e-7)
-    close("d density / dr", e_dd, dd, 1e-5 * float(dd.abs().max()) + 1e-7)
+    # the Bessel sines come from one fp64 sincos and an fp64 rotation: the remaining error is fp32 arithmetic
+    # (measured on these seeds: 3e-7 / 6e-7 of max|d|, 2.4e-7 / 8.7e-7 of max|d'|)
+    close("density", e_pk[:, 3].double(), d, 1e-6 * float(d.abs().max()) + 2e-8)
+    close("d density / dr", e_dd, dd, 2e-6 * float(dd.abs().max()) + 2e-8)
     assert torch.equal(pki[:, 1].long(), row)
     assert torch.equal(pki[:, 2].long(), xsrc)
     assert torch.equal(e_recv.long(), recv)
