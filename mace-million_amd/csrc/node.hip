@@ -116,29 +116,40 @@ extern "C" int mm_readout1(int n, const float* h1, long h_stride, const float* w
 
 // R2(h2) = sum_j w2_j silu_n(h2 . W1[:, j]) with W1 = r1_w1 / sqrt(C), w2 = r1_w2 / sqrt(16), silu_n = cst silu;
 // eat[i] += scale R2_i;  g_h2[i] = scale dR2/dh2.
-// One thread per node (hidden width H <= MM_RO2_HMAX): the weights are read at the same address by every lane
-// (scalar loads), the node's 128 features stream in as float4 and the gradient row goes out as float4.
+// Four lanes per node (hidden width H <= MM_RO2_HMAX): lane q of a node's group takes the features 4 (q + 4 j) .. + 3,
+// j = 0..7, so the group reads and writes 64 contiguous bytes per access and a lane issues its 8 loads together.
+// W1 is staged in LDS with row stride H + 1 (the 4 lanes of a group read 4 different banks).  The partial
+// pre-activations are summed over the group with two xor-shuffles, which leaves the same sum in all four lanes.
 #define MM_RO2_HMAX 32
+#define MM_RO2_NODES 64   // nodes per 256-thread workgroup
 __global__ void __launch_bounds__(256) mm_readout2_kernel(int n, const float* __restrict__ h2, long h_stride,
                                                           const float* __restrict__ W1, const float* __restrict__ w2,
                                                           int H, float cst, float scale, double* __restrict__ eat,
                                                           float* __restrict__ gh, long gh_stride) {
-  const int node = blockIdx.x * blockDim.x + threadIdx.x;
-  if (node >= n) return;
+  __shared__ float w1s[MM_C * (MM_RO2_HMAX + 1)];
+  const int ws = H + 1;
+  for (int t = threadIdx.x; t < MM_C * H; t += 256) w1s[(t / H) * ws + t % H] = W1[t];
+  __syncthreads();
+  const int node = blockIdx.x * MM_RO2_NODES + (threadIdx.x >> 2);
+  if (node >= n) return;   // the four lanes of a group share the node, so no shuffle partner is missing
+  const int q = threadIdx.x & 3;
   const floatx4* __restrict__ hp = (const floatx4*)(h2 + (size_t)node * h_stride);
+  floatx4 a[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) a[j] = hp[q + 4 * j];
   float z[MM_RO2_HMAX];
 #pragma unroll
   for (int j = 0; j < MM_RO2_HMAX; ++j) z[j] = 0.f;
-  for (int c4 = 0; c4 < MM_C / 4; ++c4) {
-    const floatx4 a = hp[c4];
-    const float* __restrict__ wr = W1 + (size_t)(4 * c4) * H;
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const float* __restrict__ wr = w1s + 4 * (q + 4 * jj) * ws;
 #pragma unroll
     for (int j = 0; j < MM_RO2_HMAX; ++j) {
       if (j < H) {
-        z[j] = fmaf(a.x, wr[j], z[j]);
-        z[j] = fmaf(a.y, wr[H + j], z[j]);
-        z[j] = fmaf(a.z, wr[2 * H + j], z[j]);
-        z[j] = fmaf(a.w, wr[3 * H + j], z[j]);
+        z[j] = fmaf(a[jj].x, wr[j], z[j]);
+        z[j] = fmaf(a[jj].y, wr[ws + j], z[j]);
+        z[j] = fmaf(a[jj].z, wr[2 * ws + j], z[j]);
+        z[j] = fmaf(a[jj].w, wr[3 * ws + j], z[j]);
       }
     }
   }
@@ -146,26 +157,29 @@ __global__ void __launch_bounds__(256) mm_readout2_kernel(int n, const float* __
 #pragma unroll
   for (int j = 0; j < MM_RO2_HMAX; ++j) {
     if (j < H) {
+      z[j] += __shfl_xor(z[j], 1);
+      z[j] += __shfl_xor(z[j], 2);
       const float sg = 1.f / (1.f + expf(-z[j]));
       e += w2[j] * cst * z[j] * sg;
       z[j] = scale * w2[j] * cst * sg * (1.f + z[j] * (1.f - sg));   // scale * d/dz (w2_j cst silu(z))
     }
   }
-  eat[node] += (double)(scale * e);
+  if (q == 0) eat[node] += (double)(scale * e);
   floatx4* __restrict__ op = (floatx4*)(gh + (size_t)node * gh_stride);
-  for (int c4 = 0; c4 < MM_C / 4; ++c4) {
-    const float* __restrict__ wr = W1 + (size_t)(4 * c4) * H;
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) {
+    const float* __restrict__ wr = w1s + 4 * (q + 4 * jj) * ws;
     floatx4 g = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < MM_RO2_HMAX; ++j) {
       if (j < H) {
         g.x = fmaf(z[j], wr[j], g.x);
-        g.y = fmaf(z[j], wr[H + j], g.y);
-        g.z = fmaf(z[j], wr[2 * H + j], g.z);
-        g.w = fmaf(z[j], wr[3 * H + j], g.w);
+        g.y = fmaf(z[j], wr[ws + j], g.y);
+        g.z = fmaf(z[j], wr[2 * ws + j], g.z);
+        g.w = fmaf(z[j], wr[3 * ws + j], g.w);
       }
     }
-    op[c4] = g;
+    op[q + 4 * jj] = g;
   }
 }
 
@@ -174,8 +188,8 @@ extern "C" int mm_readout2(int n, const float* h2, long h_stride, const float* W
   MM_CHECK_ARG(n >= 0 && H >= 1 && H <= MM_RO2_HMAX, "bad sizes (1 <= H <= 32)");
   MM_CHECK_ARG(h_stride % 4 == 0 && gh_stride % 4 == 0, "row strides must be multiples of 4 floats");
   if (n == 0) return MM_OK;
-  hipLaunchKernelGGL(mm_readout2_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, n, h2, h_stride, W1, w2, H,
-                     cst, scale, eat, gh, gh_stride);
+  hipLaunchKernelGGL(mm_readout2_kernel, dim3((n + MM_RO2_NODES - 1) / MM_RO2_NODES), dim3(256), 0, stream, n, h2,
+                     h_stride, W1, w2, H, cst, scale, eat, gh, gh_stride);
   return mm::launch_status("mm_readout2");
 }
 
