@@ -177,6 +177,9 @@ class FastLayers:
         self.dens = [(ctypes.c_float * sp.num_bessel)(*(P[f"i{k}_dens"][:, 0] / math.sqrt(sp.num_bessel)).tolist())
                      for k in range(2)]
         self.scale, self.shift = sp.scale, sp.shift
+        # pass C's loss scale R1 + G1r . h1 has the h1-gradient G1r + scale w0 on the 0e block; through p0_lin^T the
+        # constant part is the row scale w0 p0_lin[0]^T, added to gB after the linear has read G1r itself
+        self.ro1_gB = (self.scale * (P["r0"] / math.sqrt(C)) @ pl1[0].T).to(**f32).contiguous()
         self.e0 = model.e0.detach().to(dev, torch.float64)
         # -------- spline tables (fp64 sampling on the GPU)
         self.M, self.r_lo, self.r_hi = int(spline_grid), float(r_lo), sp.r_max
@@ -421,9 +424,9 @@ class FastLayers:
             h1, Mc, rho = H1[g.a:g.b], cache["M"][g.a:g.b], cache["rho"][g.a:g.b]
             self._geometry(0, g)
         D1 = 4 * C
-        K.mm_readout1(g.nC, h1, D1, self.r0s, self.scale, eat[g.a:g.b], G1r[g.a:g.b], D1, ws["gh"], D1, D1,
-                      stream())
-        self._lin(self.plan_p1, ws["gh"], D1, ws["gB"], D1, self.W_p1T, g.nC)
+        K.mm_readout1(g.nC, h1, D1, self.r0s, self.scale, eat[g.a:g.b], None, 0, None, 0, D1, stream())
+        self._lin(self.plan_p1, G1r[g.a:g.b], D1, ws["gB"], D1, self.W_p1T, g.nC)
+        ws["gB"].view(-1, D1)[:g.nC, :C].add_(self.ro1_gB)
         self._timed("symc1_bwd", (g.nC,), K.mm_symc1_bwd, g.nC, Mc, 16 * C, ws["spec"], self.Wsc1, ws["gB"], D1,
                     ws["gM"], 16 * C, rho, ws["g_rho"], stream())
         if self.ace:
