@@ -278,12 +278,13 @@ class ReceiverChunkMACE:
         gx = self._graph_exec(fl, sysm, graphs) if self.use_graphs else None
         nC = self.chunk
         cache = None
+        # pass A writes every column of every receiver's h1 row, and pass B stores every pair force of its chunk
+        # before pass C adds to it: neither buffer is cleared first (G1 and eat are accumulated into and are)
         if gx is not None:      # the executor's static buffers: its graphs read and write them in place
             H1, G1, eat = gx.H1x[:N], gx.G1[:N], gx.eat[:N]
-            H1.zero_()
             cache = gx.cache()
         else:
-            H1 = torch.zeros(N, self.D1, dtype=torch.float32, device=dev)
+            H1 = torch.empty(N, self.D1, dtype=torch.float32, device=dev)
             if self.cache_layer1:
                 if self._cache is None or self._cache["rho"].numel() < N:
                     self._cache = fl.layer1_cache(N)
@@ -302,7 +303,7 @@ class ReceiverChunkMACE:
         else:
             G1 = torch.zeros_like(H1)
             eat = torch.zeros(N, dtype=torch.float64, device=dev)
-        PF = torch.zeros(max(E, 1), 3, dtype=torch.float32, device=dev)
+        PF = torch.empty(max(E, 1), 3, dtype=torch.float32, device=dev)
         for g in graphs:
             if gx is not None and g.nC == nC:
                 gx.pass_b(g)
