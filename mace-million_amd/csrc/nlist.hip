@@ -360,7 +360,7 @@ extern "C" int mm_nl_fill(const double* pos_s, const int* cell_s, long N, const 
 
 // Per-step pair list of an MD run: the pairs of a skin list (built with r_cut = r_max + skin) whose current
 // minimum-image distance is below r_max, in the skin list's order (the same test as mm_nl_pairs_kernel).
-// One wave per receiver: 64 candidates per step, kept ones compacted in order with a ballot and a prefix popcount.
+// One wave per receiver: 256 candidates per step, kept ones compacted in order with ballots and prefix popcounts.
 // FILL = false: NN[i] = number of skin pairs of atom i within r_max; with flags != nullptr also flags[e] = 0 (kept)
 // or -1 per skin pair.  FILL = true: the kept pairs in candidate order, send[rowptr[i] + k], and fidx[e] = the
 // filtered index of skin pair e or -1; with FROM_FLAGS the keep decisions are read from fidx (the count pass's
@@ -383,32 +383,50 @@ __global__ void __launch_bounds__(256) mm_nl_filter_kernel(const double* __restr
   const long end = rp_s[i + 1];
   long n = 0;
   const long base = FILL ? rowptr[i] : 0;
-  for (long e0 = rp_s[i]; e0 < end; e0 += 64) {
-    const long e = e0 + lane;
-    bool keep = false;
-    int j = 0;
-    if (e < end) {
-      j = send_s[e];
-      if (FROM_FLAGS) {
-        keep = fidx[e] >= 0;
-      } else {
+  // 4 x 64 candidates per step: their loads are issued together (a lane past the row reads the row's last
+  // candidate and keeps nothing), then the kept ones are compacted in candidate order, 64 at a time
+  for (long e0 = rp_s[i]; e0 < end; e0 += 256) {
+    int j[4];
+    bool keep[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) j[k] = send_s[min(e0 + lane + 64 * k, end - 1)];
+    if (FROM_FLAGS) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int flag = fidx[min(e0 + lane + 64 * k, end - 1)];
+        keep[k] = (e0 + lane + 64 * k < end) & (flag >= 0);
+      }
+    } else {
+      double px[4], py[4], pz[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        px[k] = pos[3 * (long)j[k]];
+        py[k] = pos[3 * (long)j[k] + 1];
+        pz[k] = pos[3 * (long)j[k] + 2];
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
 #pragma clang fp contract(off)
-        const double dx = mm_mic(xi - pos[3 * (long)j], bx);
-        const double dy = mm_mic(yi - pos[3 * (long)j + 1], by);
-        const double dz = mm_mic(zi - pos[3 * (long)j + 2], bz);
+        const double dx = mm_mic(xi - px[k], bx);
+        const double dy = mm_mic(yi - py[k], by);
+        const double dz = mm_mic(zi - pz[k], bz);
         const double dd = (dx * dx + dy * dy) + dz * dz;
-        keep = dd < r2 && j != i;
+        keep[k] = (e0 + lane + 64 * k < end) & (dd < r2) & (j[k] != i);
       }
     }
-    const unsigned long long m = __ballot(keep);
-    if (FILL) {
-      const long slot = base + n + __popcll(m & ((1ull << lane) - 1ull));
-      if (keep) send[slot] = j;
-      if (fidx && e < end) fidx[e] = keep ? (int)slot : -1;
-    } else if (fidx && e < end) {
-      fidx[e] = keep ? 0 : -1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const long e = e0 + lane + 64 * k;
+      const unsigned long long m = __ballot(keep[k]);
+      if (FILL) {
+        const long slot = base + n + __popcll(m & ((1ull << lane) - 1ull));
+        if (keep[k]) send[slot] = j[k];
+        if (fidx && e < end) fidx[e] = keep[k] ? (int)slot : -1;
+      } else if (fidx && e < end) {
+        fidx[e] = keep[k] ? 0 : -1;
+      }
+      n += __popcll(m);
     }
-    n += __popcll(m);
   }
   if (!FILL && lane == 0) NN[i] = (int)n;
 }
