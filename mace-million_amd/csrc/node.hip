@@ -317,13 +317,28 @@ __global__ void __launch_bounds__(256) mm_pair_forces_skin_kernel(long n, const 
   if (i >= n) return;
   const int lane = threadIdx.x & 63;
   double fx = 0, fy = 0, fz = 0;
-  for (long e = skin_rowptr[i] + lane; e < skin_rowptr[i + 1]; e += 64) {
-    const int f = fidx[e];
-    if (f >= 0) {
-      const long r = fidx[rev[e]];
-      fx += (double)pf[3 * r] - (double)pf[3 * (long)f];
-      fy += (double)pf[3 * r + 1] - (double)pf[3 * (long)f + 1];
-      fz += (double)pf[3 * r + 2] - (double)pf[3 * (long)f + 2];
+  const long e1 = skin_rowptr[i + 1];
+  // 4 x 64 skin pairs per step, each level of the chain fidx[e] -> rev[e] -> fidx[rev[e]] -> the two pair forces
+  // loaded together.  A lane past the row or on a dropped pair reads the row's first entries (one shared address,
+  // not a random one) and adds exactly 0, so the sums run in the same order as one pair at a time.
+  for (long eb = skin_rowptr[i]; eb < e1; eb += 256) {
+    int f[4], r[4];
+    bool use[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) f[k] = fidx[min(eb + lane + 64 * k, e1 - 1)];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      use[k] = (eb + lane + 64 * k < e1) & (f[k] >= 0);
+      r[k] = rev[use[k] ? eb + lane + 64 * k : eb];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = fidx[r[k]];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const long a = use[k] ? f[k] : 0, b = use[k] ? max(r[k], 0) : 0;   // r >= 0 when f >= 0 (symmetric test)
+      fx += (double)pf[3 * b] - (double)pf[3 * a];
+      fy += (double)pf[3 * b + 1] - (double)pf[3 * a + 1];
+      fz += (double)pf[3 * b + 2] - (double)pf[3 * a + 2];
     }
   }
   for (int o = 32; o >= 1; o >>= 1) {
