@@ -185,7 +185,10 @@ int mm_linear(const float* in, long in_stride, const int* in_rows, float* out, l
               mm_stream_t stream);
 int mm_species_lists(const int* spec, int n, int S, int* lists, long stride, int* counts, mm_stream_t stream);
 /* readouts with energy accumulation and gradient: model.readouts[0] / [1] and the losses of passes B and C
- * (mliap_threepass.py:550, 578-579) */
+ * (mliap_threepass.py:550, 578-579).  mm_readout1: eat[i] += scale h1[i, 0:128] . w0 and, when gh is not null,
+ * gh[i, j] = g1r[i, j] + scale w0[j] (j < 128) or g1r[i, j] (128 <= j < D); g1r and gh null = energies only; D >= 128.
+ * mm_readout2: eat[i] += scale R2(h2[i]) and gh[i] = scale dR2/dh2 (128 values), 1 <= H <= 32, both row strides
+ * multiples of 4 floats. */
 int mm_readout1(int n, const float* h1, long h_stride, const float* w0, float scale, double* eat, const float* g1r,
                 long g1_stride, float* gh, long gh_stride, int D, mm_stream_t stream);
 int mm_readout2(int n, const float* h2, long h_stride, const float* W1, const float* w2, int H, float cst,
