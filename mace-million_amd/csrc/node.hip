@@ -273,34 +273,48 @@ extern "C" int mm_gather_rows_csr(const int* rowptr, const int* idx, const float
 // F[i] = - sum_{e in row(i)} PF_e + sum_{e : send(e) = i} PF_e with v_e = x_recv - x_send (the reference's
 // _accum_forces, receiver_chunk_mace.py:272-276).  Receiver part: CSR over the receiver-sorted pairs; sender
 // part: CSR over the pairs sorted by sender (s_perm lists pair ids per sender).  fp64 accumulation.
-__global__ void mm_pair_forces_to_atoms_kernel(int n, const long* __restrict__ rowptr, const long* __restrict__ s_rowptr,
-                                               const long* __restrict__ s_perm, const float* __restrict__ pf,
-                                               double* __restrict__ F) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+// One wave per atom: the lanes stride over the atom's pairs as receiver (-PF) and as sender (+PF, through the
+// sender CSR), fp64 sums per lane, then a fixed xor butterfly over the wave (repeated runs give identical sums).
+__global__ void __launch_bounds__(256) mm_pair_forces_to_atoms_kernel(int n, const long* __restrict__ rowptr,
+                                                                      const long* __restrict__ s_rowptr,
+                                                                      const long* __restrict__ s_perm,
+                                                                      const float* __restrict__ pf,
+                                                                      double* __restrict__ F) {
+  const long i = blockIdx.x * 4L + (threadIdx.x >> 6);
   if (i >= n) return;
+  const int lane = threadIdx.x & 63;
   double fx = 0, fy = 0, fz = 0;
-  for (long e = rowptr[i]; e < rowptr[i + 1]; ++e) {
+  const long r1 = rowptr[i + 1];
+  for (long e = rowptr[i] + lane; e < r1; e += 64) {
     fx -= pf[3 * e];
     fy -= pf[3 * e + 1];
     fz -= pf[3 * e + 2];
   }
-  for (long k = s_rowptr[i]; k < s_rowptr[i + 1]; ++k) {
+  const long s1 = s_rowptr[i + 1];
+  for (long k = s_rowptr[i] + lane; k < s1; k += 64) {
     const long e = s_perm[k];
     fx += pf[3 * e];
     fy += pf[3 * e + 1];
     fz += pf[3 * e + 2];
   }
-  F[3 * (size_t)i] = fx;
-  F[3 * (size_t)i + 1] = fy;
-  F[3 * (size_t)i + 2] = fz;
+  for (int o = 32; o >= 1; o >>= 1) {
+    fx += __shfl_xor(fx, o);
+    fy += __shfl_xor(fy, o);
+    fz += __shfl_xor(fz, o);
+  }
+  if (lane == 0) {
+    F[3 * i] = fx;
+    F[3 * i + 1] = fy;
+    F[3 * i + 2] = fz;
+  }
 }
 
 extern "C" int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* s_rowptr, const long* s_perm,
                                        const float* pf, double* F, hipStream_t stream) {
   MM_CHECK_ARG(n >= 0, "bad sizes");
   if (n == 0) return MM_OK;
-  hipLaunchKernelGGL(mm_pair_forces_to_atoms_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, n, rowptr,
-                     s_rowptr, s_perm, pf, F);
+  hipLaunchKernelGGL(mm_pair_forces_to_atoms_kernel, dim3((unsigned)((n + 3L) / 4)), dim3(256), 0, stream, n,
+                     rowptr, s_rowptr, s_perm, pf, F);
   return mm::launch_status("mm_pair_forces_to_atoms");
 }
 
