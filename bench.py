@@ -219,9 +219,9 @@ def kernel_table(fl, ktimes, steps):
 
 
 def roofline_of(kernels, workload=None):
-    """Roofline of the dominant kernel (most time per step): the compute roof of the unit it runs on (VALU 78.6,
-    fp32 MFMA 157.3 TFLOP/s) when its intensity is above that unit's ridge with 8 TB/s, the HBM roof below it.
-    Both the HBM and the compute figures are reported."""
+    """Roofline of the dominant kernel (most time per step): the compute roof of the unit it runs on (fp32 VALU
+    157.3 TFLOP/s with gfx950's dual issue, fp32 MFMA 157.3 TFLOP/s) when its intensity is above that unit's ridge
+    with 8 TB/s, the HBM roof below it.  Both the HBM and the compute figures are reported."""
     if not kernels:
         return None
     dom = max(kernels, key=lambda k: kernels[k]["ms_per_step"])

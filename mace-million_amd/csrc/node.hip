@@ -108,6 +108,7 @@ __global__ void mm_readout1_kernel(int n, const float* __restrict__ h1, long h_s
 extern "C" int mm_readout1(int n, const float* h1, long h_stride, const float* w0, float scale, double* eat,
                            const float* g1r, long g1_stride, float* gh, long gh_stride, int D, hipStream_t stream) {
   MM_CHECK_ARG(n >= 0 && D >= MM_C, "bad sizes");
+  MM_CHECK_ARG((gh == nullptr) == (g1r == nullptr), "g1r and gh must both be given (gradient mode) or both be null");
   if (n == 0) return MM_OK;
   hipLaunchKernelGGL(mm_readout1_kernel, dim3((n + 3) / 4), dim3(256), 0, stream, n, h1, h_stride, w0, scale, eat,
                      g1r, g1_stride, gh, gh_stride, D);
@@ -333,8 +334,10 @@ __global__ void __launch_bounds__(256) mm_pair_forces_skin_kernel(long n, const 
   double fx = 0, fy = 0, fz = 0;
   const long e1 = skin_rowptr[i + 1];
   // 4 x 64 skin pairs per step, each level of the chain fidx[e] -> rev[e] -> fidx[rev[e]] -> the two pair forces
-  // loaded together.  A lane past the row or on a dropped pair reads the row's first entries (one shared address,
-  // not a random one) and adds exactly 0, so the sums run in the same order as one pair at a time.
+  // loaded together.  A lane past the row or on a dropped pair reads the row's first entries and pf row 0 (one
+  // shared address, not a random one; pf holds at least one row) and adds 0.0 through a select, so an unwritten
+  // pf row 0 (no pair survived the filter) cannot reach the sums, which run in the same order as one pair at a
+  // time.
   for (long eb = skin_rowptr[i]; eb < e1; eb += 256) {
     int f[4], r[4];
     bool use[4];
@@ -350,9 +353,12 @@ __global__ void __launch_bounds__(256) mm_pair_forces_skin_kernel(long n, const 
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const long a = use[k] ? f[k] : 0, b = use[k] ? max(r[k], 0) : 0;   // r >= 0 when f >= 0 (symmetric test)
-      fx += (double)pf[3 * b] - (double)pf[3 * a];
-      fy += (double)pf[3 * b + 1] - (double)pf[3 * a + 1];
-      fz += (double)pf[3 * b + 2] - (double)pf[3 * a + 2];
+      const double dx = (double)pf[3 * b] - (double)pf[3 * a];
+      const double dy = (double)pf[3 * b + 1] - (double)pf[3 * a + 1];
+      const double dz = (double)pf[3 * b + 2] - (double)pf[3 * a + 2];
+      fx += use[k] ? dx : 0.0;
+      fy += use[k] ? dy : 0.0;
+      fz += use[k] ? dz : 0.0;
     }
   }
   for (int o = 32; o >= 1; o >>= 1) {

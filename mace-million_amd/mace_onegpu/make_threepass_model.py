@@ -53,7 +53,7 @@ def main(argv=None):
     a = ap.parse_args(argv)
     obj = make(a.out, a.seed, a.weights, a.chunk, a.spline_grid, a.recipe)
     print(f"saved {a.out}: chunk={obj.chunk} spline_grid={obj.spline_grid} dtype={obj.dtype} "
-          f"elements={len(obj.element_types)} recipe={obj._recipe is not None}")
+          f"elements={len(obj.element_types)} recipe={obj._rebuild is not None}")
 
 
 if __name__ == "__main__":

@@ -233,6 +233,16 @@ class _Runtime:
         self.gx = None
         self.n_captures = 0
         self.log = open(k.log_path, "a", buffering=1) if k.log_path else None
+        self.peak = 0.0                                   # running maximum of peak_out over the logged calls
+
+    def peak_gb(self):
+        """Peak device allocation (GB) since the previous logged call, and the running maximum over calls (the
+        reference's peak_out / peak_gb, mliap_threepass.py:433-441).  Only with the per-call log on: reading
+        resets torch's peak counter."""
+        p = torch.cuda.max_memory_allocated(self.dev) / 1e9
+        torch.cuda.reset_peak_memory_stats(self.dev)
+        self.peak = max(self.peak, p)
+        return round(p, 3), round(self.peak, 3)
 
     def covers(self, elems):
         return set(torch.unique(elems).tolist()) <= set(self.cols)
@@ -362,10 +372,10 @@ class ThreePassMLIAP(MLIAPUnified):
         self.step = 0
         self.profile = False            # per-pass wall times in last_timings (synchronises after every pass)
         self.last_timings = None
-        self._recipe = None
+        self._rebuild = None            # the reference's attribute name: model files carry the recipe under it
         if rebuild_config is not None:
             state = {k: v.detach().cpu() for k, v in model.state_dict().items()}
-            self._recipe = (type(model), dict(rebuild_config), state)
+            self._rebuild = (type(model), dict(rebuild_config), state)
         self._rt = None
 
     @property
@@ -377,17 +387,25 @@ class ThreePassMLIAP(MLIAPUnified):
     def __getstate__(self):
         """Only the constructor's state travels in the model file; with a recipe the module itself stays out."""
         state = {k: v for k, v in self.__dict__.items() if k not in ("_rt", "last_timings")}
-        if self._recipe is not None:
+        if state.get("_rebuild") is not None:
             state.pop("model", None)
         return state
 
     def __setstate__(self, state):
+        """Accepts the reference's layout (recipe under `_rebuild`, mliap_threepass.py:173-184) and files that
+        stored the recipe under `_recipe`."""
+        state = dict(state)
+        legacy = state.pop("_recipe", None)
+        if state.get("_rebuild") is None:
+            state["_rebuild"] = legacy
         self.__dict__.update(state)
         self._rt = None
         self.last_timings = None
 
     def _rebuild_model(self):
-        cls, kwargs, state = self._recipe
+        if getattr(self, "_rebuild", None) is None:
+            raise RuntimeError("ThreePassMLIAP: the model file holds neither the model nor a rebuild recipe")
+        cls, kwargs, state = self._rebuild
         m = cls(**kwargs)
         m.load_state_dict(state, strict=True)
         return m.to(self.dtype)
@@ -426,9 +444,12 @@ class ThreePassMLIAP(MLIAPUnified):
         data.update_pair_forces_gpu(PF)
         self.last_timings = timings
         if rt.log is not None:
+            peak_out, peak_gb = rt.peak_gb()
             rt.log.write(json.dumps(dict(step=self.step, nlocal=nl, ntotal=nt, npairs=P, chunks=n_chunks,
                                          sorted_pairs=batch.perm is None, graphs=rt.gx is not None,
-                                         t_total=time.perf_counter() - t_call, **timings)) + "\n")
+                                         captures=rt.n_captures, e_cap=rt.gx.e_cap if rt.gx is not None else None,
+                                         t_total=time.perf_counter() - t_call, **timings,
+                                         peak_out=peak_out, peak_gb=peak_gb)) + "\n")
 
     def compute_descriptors(self, data):
         pass

@@ -68,15 +68,22 @@ def test_mliap_is_bitwise_repeatable(model, water, graphs, monkeypatch):
         assert tp._rt.gx is not None and tp._rt.gx.n_replays > 0
 
 
-def test_md_trajectory_is_bitwise_repeatable(model):
+@pytest.mark.parametrize("graphs", [False, True])
+def test_md_trajectory_is_bitwise_repeatable(model, graphs):
+    """Eager, and with HIP graphs: chunk 512 gives 3 full chunks of the 1,536 atoms, captured once and replayed with
+    the persistent MD chunk objects (their sender CSR reloaded into the graph slots on every step)."""
     from mace_onegpu import systems
     from mace_onegpu.md import MDRunner
     pos, box, Z = systems.water_box(512, seed=6)
     runs = []
     for rep in range(2):
-        _say(f"case md deterministic run {rep}")
-        md = MDRunner(model, pos, box, Z, chunk=700, device="cuda", deterministic=True)
+        _say(f"case md deterministic graphs={graphs} run {rep}")
+        md = MDRunner(model, pos, box, Z, chunk=512 if graphs else 700, device="cuda", deterministic=True,
+                      use_graphs=graphs)
         for _ in range(4):
             md.step()
+        if graphs:
+            gx = md.ev._gx
+            assert gx is not None and gx.n_replays > 0
         runs.append((md.pos.clone(), md.vel.clone(), md.E))
     assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1]) and runs[0][2] == runs[1][2]

@@ -127,3 +127,31 @@ def test_md_with_graphs_matches_eager(model):
         assert abs(a.E - b.E) < 1e-9 * len(pos)
         assert dx < 1e-9
     assert b.ev.n_captures >= 1 and b.ev._gx.n_replays > 0
+
+
+def test_mliap_call_log_fields(model, water_sys, tmp_path, monkeypatch):
+    """MACE3P_LOG: one JSON line per call with the reference's fields (mliap_threepass.py:433-441, 606-616): sizes,
+    chunks, captures, e_cap, the phase times, peak_out (peak device GB of this call) and peak_gb (running max); a
+    capture line precedes the first graphed call."""
+    import json
+
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    s = water_sys
+    log = tmp_path / "m3p.jsonl"
+    monkeypatch.setenv("MACE3P_LOG", str(log))
+    monkeypatch.setenv("MACE3P_GRAPHS", "1")
+    tp = ThreePassMLIAP(model, chunk=48)
+    for call in range(2):
+        _say(f"case mliap log call {call}")
+        tp.compute_forces(PeriodicMLIAPData(s, s.spidx.long(), ghosts=True))
+    tp._rt.log.flush()
+    lines = [json.loads(x) for x in log.read_text().splitlines()]
+    calls = [x for x in lines if "step" in x]
+    assert "capture" in lines[0] and len(calls) == 2
+    for c in calls:
+        assert c["nlocal"] == s.N and c["chunks"] == 4 and c["graphs"] and c["captures"] == 1
+        assert c["e_cap"] >= max(1, int(s.rowptr[-1]) // 4)
+        assert {"A", "B", "C", "t_total"} <= set(c)
+        assert 0 < c["peak_out"] <= c["peak_gb"]
+    assert calls[1]["peak_gb"] == max(calls[0]["peak_gb"], calls[1]["peak_out"])

@@ -76,3 +76,17 @@ def test_codegen_term_coverage():
         assert len(re.findall(r"acc\d+" + sfx + r" = fmaf\(", fwd2)) == len(t.tp2["terms"])
     fwd1 = open(os.path.join(gen, "conv_l1.hip")).read().split("mm_conv1_bwd_kernel")[0]
     assert len(re.findall(r"acc\d+ = fmaf\(", fwd1)) == len(t.tp1["terms"])
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (python mace-million_amd/build.py)")
+def test_readout1_refuses_half_gradient_mode():
+    """mm_readout1 computes energies only when g1r and gh are both null and the gradient when both are given; one
+    without the other is refused on the host with MM_EINVAL before any launch (the pointers are never read)."""
+    from mace_onegpu import _lib
+    so = _lib.lib()
+    fake = ctypes.c_void_p(0x1000)      # never dereferenced: the argument check returns first
+    null = ctypes.c_void_p(0)
+    for g1r, gh in ((null, fake), (fake, null)):
+        rc = so.mm_readout1(4, fake, 512, fake, 1.0, fake, g1r, 512, gh, 512, 512, null)
+        assert rc == -1
+        assert "g1r and gh" in _lib.last_error()

@@ -41,8 +41,35 @@ def test_rebuild_recipe(tmp_path):
     out = tmp_path / "m3pr.pt"
     obj = make_threepass_model.make(str(out), seed=3, recipe=True)
     back = torch.load(str(out), weights_only=False)
-    assert "model" not in back.__dict__ and back._recipe is not None
+    assert "model" not in back.__dict__ and back._rebuild is not None
     assert _same_weights(back._rebuild_model(), obj.model)
+
+
+@pytest.mark.parametrize("key", ["_rebuild", "_recipe"])
+def test_recipe_state_layouts(key):
+    """A state dict with the recipe under the reference's `_rebuild` (mliap_threepass.py:173-184), or under the
+    `_recipe` key an earlier file layout used, and no model: the model is rebuilt and the object pickles again."""
+    src = make_threepass_model.MaceModel(seed=5)
+    obj = ThreePassMLIAP(src, rebuild_config=dict(seed=5))
+    state = obj.__getstate__()
+    assert "model" not in state and state["_rebuild"] is not None
+    state[key] = state.pop("_rebuild")
+    back = ThreePassMLIAP.__new__(ThreePassMLIAP)
+    back.__setstate__(state)
+    assert back._rebuild is not None and "_recipe" not in back.__dict__
+    assert _same_weights(back._rebuild_model(), src)
+    again = pickle.loads(pickle.dumps(back))
+    assert "model" not in again.__dict__ and _same_weights(again._rebuild_model(), src)
+
+
+def test_missing_model_and_recipe_raises():
+    obj = ThreePassMLIAP(make_threepass_model.MaceModel(seed=2))
+    state = obj.__getstate__()
+    state.pop("model")
+    back = ThreePassMLIAP.__new__(ThreePassMLIAP)
+    back.__setstate__(state)
+    with pytest.raises(RuntimeError, match="neither the model nor a rebuild recipe"):
+        back._rebuild_model()
 
 
 def test_weights_file(tmp_path):
