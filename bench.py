@@ -1,7 +1,7 @@
 #!/usr/bin/env python
 """Benchmark of the MI355X three-pass MACE path on one GPU (benchmark configurations 2-5).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5|4|3|2] [--no-cpu] [--graphs]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 5|4|3|2|1] [--no-cpu] [--graphs]
 
 Prints ONE JSON line.  Default: configuration 5, the metric's "1M-atom water" -- 343,000 rigid H2O molecules
 (1,029,000 atoms) at 1.0 g/cm^3, random-init MPA-0-medium architecture, fp32 kernels, velocity-Verlet MD (dt 0.5 fs,
@@ -15,6 +15,8 @@ force call, then K timed steps between synchronisations.
   --config 2 : edge-convolution microbenchmark on one 16,384-receiver chunk of the config-3 box with synthetic edge
                vectors (unit directions x U[0.8, 6.0] A), features and cotangents; value = achieved algorithmic GB/s of
                the layer-2 forward kernel, every kernel listed
+  --config 1 : the 192-atom water box through ThreePassMLIAP.compute_forces (periodic-image ghosts), one E+F per
+               step, with the fp64 CPU restatement's E+F (median of 3) and the GPU-vs-CPU energy and force deviations
 Objects beside the contract fields:
   roofline     : the dominant kernel, algorithmic bytes (or FLOPs) per launch / mean launch time measured with HIP
                  events on the launch stream (during the timed steps; with graphs, in one eager step after them).  bound: "valu" for the edge convolutions (fp32
@@ -26,11 +28,14 @@ Objects beside the contract fields:
                  HIP events in one extra step after the timed ones
   step_roofline: atom-steps/s against the fp32 ceiling of the exact model's work per atom-step (edge terms, node
                  linears, and the symmetric contractions at the operations the kernels execute)
-  cpu_baseline : the fp32 torch-CPU restatement of the production three-pass algorithm (oracle/cpu_fp32.py: spline
-                 tables, passes A / B / C) timed on one 16,384-receiver chunk of the same system and extrapolated to
-                 all chunks, in the metric's unit
-  configs      : (default run) configurations 3, 4 and 2 measured in the same process after configuration 5, each
-                 with its value, dominant-kernel roofline and per-kernel table
+  cpu_baseline : configs 3-5: the fp32 torch-CPU restatement of the production three-pass algorithm
+                 (oracle/cpu_fp32.py: spline tables, passes A / B / C) timed on one 16,384-receiver chunk of that
+                 configuration's own system and extrapolated to all its chunks, in the metric's unit; config 2: the
+                 restatement's layer-2 convolution forward and backward on 2,048 receivers of the chunk with the GPU
+                 run's inputs, scaled to the chunk (and the GPU kernels' outputs checked against it); config 1: the
+                 fp64 restatement on the whole box, median of 3
+  configs      : (default run) configurations 3, 4, 2 and 1 measured in the same process after configuration 5, each
+                 with its value, dominant-kernel roofline, per-kernel table and CPU baseline
 """
 import argparse
 import json
@@ -316,10 +321,13 @@ def cpu_baseline_chunk(pos, box, spec, NN, send, chunk=16384, label=""):
                 extrapolated=True, seconds_per_chunk=round(t_chunk, 2))
 
 
-def cpu_baseline_conv(rij, recv_local, ls, rowptr, E_full, nC_full, nN_full, n_recv=512):
+def cpu_baseline_conv(rij, recv_local, ls, rowptr, E_full, nC_full, nN_full, X_gpu, gA_gpu, n_recv=2048):
     """fp32 torch-CPU layer-2 edge convolution of the restatement (512-knot table lookup of W, channelwise TP over
-    the sparse path table, receiver sum) on the first n_recv receivers of the config-2 chunk, scaled to the chunk's
-    edges and expressed in the metric's unit (algorithmic GB/s of mm_conv2_fwd over the whole chunk)."""
+    the sparse path table, receiver sum), forward and backward (autograd: dL/dvec and dL/dX for L = gA . out, as
+    the reference's conv_spline._bench times both, conv_spline.py:304-455), on the first n_recv receivers of the
+    config-2 chunk with the GPU run's own sender features X and cotangent gA.  The times are scaled to the chunk's
+    edges; the value is the forward's algorithmic GB/s of mm_conv2_fwd over the whole chunk (the metric's unit).
+    Returns (baseline dict, (out [n_recv, 40, C], dL/dvec [ne, 3], dL/dX [n, 4, C])) for the in-bench check."""
     import torch
 
     sys.path.insert(0, ROOT)
@@ -332,26 +340,107 @@ def cpu_baseline_conv(rij, recv_local, ls, rowptr, E_full, nC_full, nN_full, n_r
     t32 = mace_ref.Tables64(m, [0, 7], n_grid=512).astype(torch.float32)
     d = ChannelwiseTP([0, 1])
     ne = int(rowptr[n_recv])
-    vec = torch.as_tensor(rij[:ne]).float()
+    vec = torch.as_tensor(rij[:ne]).float().requires_grad_(True)
     lr = torch.as_tensor(recv_local[:ne]).long()
     send = torch.as_tensor(ls[:ne]).long()
     n = int(send.max()) + 1
-    X = torch.randn(n, d.nX, C, generator=torch.Generator().manual_seed(2))
+    X = torch.as_tensor(X_gpu[:n]).float().reshape(n, d.nX, C).clone().requires_grad_(True)
+    G = torch.as_tensor(gA_gpu[:n_recv]).float().reshape(n_recv, d.nO, C)
     pair = torch.zeros(ne, dtype=torch.long)
     t0 = time.perf_counter()
     r = torch.linalg.vector_norm(vec, dim=1)
     W = t32.lookup(1, r, pair).reshape(ne, d.nW, C)
     Y = mace_ref.sh(vec)
     mid = mace_ref.channelwise_tp(W, X, Y, send, d.table["paths"], d.table["in_ls"], o3.coupling)
-    mace_ref.scatter_sum(mid, lr, n_recv)
-    dt = time.perf_counter() - t0
+    out = mace_ref.scatter_sum(mid, lr, n_recv)
+    t_fwd = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    gv, gx = torch.autograd.grad((out * G).sum(), [vec, X])
+    t_bwd = time.perf_counter() - t0
     B, _ = conv_algorithmic("conv2_fwd", E_full, nC_full, nN_full, d.table)
-    t_full = dt * E_full / ne
-    return dict(value=round(B / t_full / 1e9, 3), unit="GB/s", cores=ncores(), kind="port",
-                sample=f"fp32 torch-CPU layer-2 convolution of the restatement (table lookup of W, channelwise TP, "
-                       f"receiver sum; oracle/mace_ref.py) on the chunk's first {n_recv} receivers ({ne} edges), "
-                       f"{dt:.2f} s on {ncores()} threads, scaled to the chunk's {E_full} edges ({t_full:.1f} s); "
-                       f"bytes counted as for mm_conv2_fwd", extrapolated=True)
+    scale = E_full / ne
+    cpu = dict(value=round(B / (t_fwd * scale) / 1e9, 3), unit="GB/s", cores=ncores(), kind="port",
+               fwd_s_scaled=round(t_fwd * scale, 2), bwd_s_scaled=round(t_bwd * scale, 2),
+               sample=f"fp32 torch-CPU layer-2 convolution of the restatement (table lookup of W, channelwise TP, "
+                      f"receiver sum; oracle/mace_ref.py) on the chunk's first {n_recv} receivers ({ne} edges) with "
+                      f"the GPU run's features and cotangent: forward {t_fwd:.2f} s, backward (dL/dvec, dL/dX by "
+                      f"autograd) {t_bwd:.2f} s on {ncores()} threads, scaled to the chunk's {E_full} edges "
+                      f"({t_fwd * scale:.1f} s + {t_bwd * scale:.1f} s); bytes counted as for mm_conv2_fwd",
+               extrapolated=True)
+    return cpu, (out.detach(), gv, gx, n_recv, ne, n)
+
+
+def cpu_baseline_config1(pos, box, spec, recv, send, reps=3):
+    """Configuration 1 on the CPU as the reference evaluates it: fp64, exact radial MLP (no tables), the three-pass
+    algorithm of ReceiverChunkMACE.compute (oracle/mace_ref.py three_pass, one chunk of all 192 atoms), median wall
+    time of `reps` evaluations.  Returns (baseline dict, (E, F [N, 3])) for the GPU parity figures."""
+    import numpy as np
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from mace_onegpu import model as mm, o3
+    from oracle import mace_ref
+
+    torch.set_num_threads(ncores())
+    m = mace_ref.RefModel(mm.MaceModel(seed=0), o3.coupling)
+    N = len(pos)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        E0, _, F0, _, _ = mace_ref.three_pass(m, pos, box, spec, recv, send, chunk=N)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    return (dict(value=round(N / t, 2), unit="atom-steps/s", cores=ncores(), kind="port",
+                 sample=f"fp64 torch-CPU three-pass restatement (oracle/mace_ref.py, exact radial MLP) of the whole "
+                        f"{N}-atom box, median of {reps} E+F evaluations: {t:.2f} s on {ncores()} threads",
+                 extrapolated=False, seconds_per_step=round(t, 3)), (E0, F0))
+
+
+def run_config1(a):
+    """Configuration 1: the 64-molecule water box (192 atoms, L = 12.416 A) through the ML-IAP boundary on the GPU
+    (ThreePassMLIAP.compute_forces with periodic-image ghosts, fp32 kernels), one E+F per step, against the fp64 CPU
+    restatement timed beside it (median of 3); the GPU energies and forces are compared with it."""
+    import numpy as np
+    import torch
+
+    from mace_onegpu import model as mm, systems
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    from mace_onegpu.receiver_chunk_mace import System
+
+    pos, box, Z = systems.water_box(64, seed=0)
+    s = System(pos, box, Z - 1, 6.0, "cuda")
+    s.build_neighbors()
+    tp = ThreePassMLIAP(mm.MaceModel(seed=0))
+    data = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True)
+    for _ in range(max(a.warmup, 1)):
+        tp.compute_forces(data)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        tp.compute_forces(data)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    F = data.atom_forces().cpu()
+    E = float(data.energy)
+    cpu, parity = None, None
+    if not a.no_cpu:
+        recv = np.repeat(np.arange(s.N), s.NN.cpu().numpy())
+        cpu, (E0, F0) = cpu_baseline_config1(s.pos.cpu().numpy(), box, s.spidx.cpu().numpy(), recv,
+                                             s.send.cpu().numpy())
+        parity = {"E_gpu_eV": round(E, 9), "E_cpu_fp64_eV": round(E0, 9), "dE_per_atom_eV": abs(E - E0) / s.N,
+                  "max_abs_dF_eV_per_A": float((F - F0).abs().max()), "max_abs_F_eV_per_A": float(F0.abs().max()),
+                  "tolerance": {"dE_per_atom_eV": 1e-5, "max_abs_dF_eV_per_A": 1e-3}}
+        parity["pass"] = parity["dE_per_atom_eV"] < 1e-5 and parity["max_abs_dF_eV_per_A"] < 1e-3
+    value = s.N * a.steps / dt
+    line = base_line(a, "atom-steps/s (E+F, 192-atom water, fp32 GPU vs fp64 CPU, 1 GPU)", value,
+                     dt / a.steps * 1e3, "atom-steps/s", "synthetic (seeded water generator, random-init weights)",
+                     {"workload": "config1: 64-molecule water (192 atoms, L = 12.416 A), random-init MPA-0-medium "
+                                  "architecture, one E+F per step through ThreePassMLIAP.compute_forces with "
+                                  "periodic-image ghosts (fp32 kernels); the CPU leg is the fp64 restatement",
+                      "atoms": s.N, "ghosts": data.nghost, "pairs": data.npairs, "E_per_atom_eV": round(E / s.N, 9),
+                      "parity_vs_fp64_cpu": parity}, None, {}, cpu)
+    return line
 
 
 def exit_multi_gpu():
@@ -515,6 +604,7 @@ def run_ef(a):
         cpu = dict(a.cpu_from)
     elif not a.no_cpu:
         print(f"# cpu baseline: one 16,384-receiver chunk of configuration {a.config}", file=sys.stderr, flush=True)
+        # configuration 3 has exactly 6 such chunks, configuration 4 30.5: the extrapolation counts the chunks
         cpu = cpu_baseline_chunk(s.pos.cpu().numpy(), s.box, s.spidx.cpu().numpy(), s.NN.cpu().numpy(),
                                  s.send.cpu().numpy(), 16384, f"the configuration-{a.config} system")
     n_pairs = int(s.rowptr[-1])
@@ -643,17 +733,42 @@ def run_conv(a):
     ref = tp(X2, Yc, Wsp, ei)[:nr]
     err = float((ref - out2[:nr]).abs().max() / ref.abs().max())
     v = kernels["conv2_fwd"]
-    cpu = None
+    cpu, oracle_check = None, None
     if not a.no_cpu:
         rp_h = g.rowptr.cpu().numpy()
-        cpu = cpu_baseline_conv(g.rij.cpu().numpy(), g.recv_local.cpu().numpy(), g.ls.cpu().numpy(), rp_h, E, nC, nN)
+        cpu, (o_out, o_gv, o_gx, nr_c, ne_c, nn_c) = cpu_baseline_conv(
+            g.rij.cpu().numpy(), g.recv_local.cpu().numpy(), g.ls.cpu().numpy(), rp_h, E, nC, nN, X2.cpu(),
+            gA2.cpu())
+        # the same receivers through the GPU kernels: forward output, and the backward of L = gA . out restricted
+        # to them (gA zero elsewhere) -> dL/dX (G1 path) and per-edge dL/dvec (mm_edge_grad, no density term)
+        gAm = gA2.clone()
+        gAm[nr_c:] = 0
+        gXm = torch.zeros_like(X2)
+        partm = torch.empty_like(part)
+        PFm = torch.empty(E, 3, device="cuda")
+        K.mm_conv2_bwd(g.rowptr, nC, pk2, eu2, X2, 4 * C, fl.tab[1], fl.n_tab, fl.M, fl.inv_h, gAm, partm, E * 17,
+                       gXm, st)
+        K.mm_edge_grad(E, None, partm, E * 17, 8, torch.zeros(nC, device="cuda"), ws["e_recv"], ws["e_dd"], eu2,
+                       PFm, 0, st)
+        calls["conv2_fwd"][0]()
+        torch.cuda.synchronize()
+
+        def rel(gpu, ref):
+            return float((gpu.double().cpu() - ref.double()).abs().max() / ref.double().abs().max())
+        oracle_check = {"receivers": nr_c, "edges": ne_c, "tolerance": 1e-4,
+                        "out_max_rel": rel(out2[:nr_c].view(nr_c, 40, C), o_out),
+                        "dL_dvec_max_rel": rel(PFm[:ne_c], o_gv),
+                        "dL_dX_max_rel": rel(gXm[:nn_c].view(nn_c, 4, C), o_gx)}
+        oracle_check["pass"] = all(oracle_check[k] < 1e-4 for k in ("out_max_rel", "dL_dvec_max_rel",
+                                                                      "dL_dX_max_rel"))
     line = base_line(a, "edge-conv achieved algorithmic GB/s (layer-2 forward, one 16,384-receiver chunk)", v["GBps"],
                      v["ms_per_launch"], "GB/s",
                      "synthetic (config-3 topology; random unit directions x U[0.8, 6] A, N(0,1) features and "
                      "cotangents, spline tables of the random-init model)",
                      {"workload": "config2: edge-convolution kernels on chunk 0 (16,384 receivers) of the 98,304-atom "
                                   "water box", "edges": E, "receivers": nC, "nodes": nN,
-                      "check_vs_FusedConvTP_max_rel": err}, roofline_of(kernels), kernels, cpu)
+                      "check_vs_FusedConvTP_max_rel": err, "check_vs_oracle": oracle_check},
+                     roofline_of(kernels), kernels, cpu)
     line["steps_note"] = "steps = launches of each kernel"
     return line
 
@@ -727,13 +842,94 @@ def symc_gemm_probe():
                       "bmm_fp32_16col_TFLOPs": round(res[16][1], 2)}), flush=True)
 
 
+def replicate(pos, box, Z, reps):
+    """Periodic replica (nx, ny, nz) of a box: copy c = (ix, iy, iz) (ix slowest) holds atoms c * N .. c * N + N - 1
+    at pos + (ix, iy, iz) * box, so atom j of the replica is atom j % N of the base box."""
+    import numpy as np
+    nx, ny, nz = reps
+    sh = np.array([(ix, iy, iz) for ix in range(nx) for iy in range(ny) for iz in range(nz)], dtype=np.float64)
+    pos_r = (pos[None, :, :] + (sh * np.asarray(box))[:, None, :]).reshape(-1, 3)
+    return pos_r, np.asarray(box) * np.array(reps, dtype=np.float64), np.tile(Z, len(sh))
+
+
+def run_capacity(a):
+    """Memory and exactness at scale: the configuration-5 water box and its periodic replicas evaluated with
+    ReceiverChunkMACE (chunk 131072, eager chunks) with the pass-A layer-1 cache on and off.  Per run: peak device
+    GB (torch allocator), seconds per E+F, E/N and, for replicas, the largest deviations of per-atom energies and
+    forces from the base box's (atom j of a replica is atom j % N of the base).  resident bytes per atom = the slope
+    of peak GB against N between the base and the largest replica; the largest N on this GPU follows from that
+    line and the device's memory (what torch may allocate)."""
+    import numpy as np
+    import torch
+
+    from mace_onegpu import model as mm, systems
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+    pos, box, Z = systems.water_box(a.n_mol, seed=0)
+    model = mm.MaceModel(seed=0)
+    reps = [tuple(int(x) for x in r.split("x")) for r in a.capacity.split(",")]
+    runs, base = [], {}
+
+    def one(rp, cache, rec):
+        n_rep = rp[0] * rp[1] * rp[2]
+        p_r, b_r, z_r = replicate(pos, box, Z, rp) if n_rep > 1 else (pos, box, Z)
+        rec["atoms"] = len(p_r)
+        s = System(p_r, b_r, z_r - 1, 6.0, "cuda")
+        s.build_neighbors()
+        ev = ReceiverChunkMACE(model, chunk=a.chunk or 131072, device="cuda", cache_layer1=cache)
+        ev.compute(s)                  # set-up call (tables, workspaces)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        E, eat, F, PF = ev.compute(s)
+        torch.cuda.synchronize()
+        rec.update(pairs=int(s.rowptr[-1]), s_per_EF=round(time.perf_counter() - t0, 4), E_per_atom_eV=E / s.N,
+                   peak_GB=round(torch.cuda.max_memory_allocated() / 1e9, 3))
+        perm = s.perm.long()
+        Fo = torch.empty_like(F)
+        Fo[perm] = F
+        eo = torch.empty_like(eat)
+        eo[perm] = eat
+        if n_rep == 1:
+            base[cache] = (E / s.N, Fo.cpu(), eo.cpu())
+        elif cache in base:
+            E0, F0, e0 = base[cache]
+            rec.update(dE_per_atom_vs_base=abs(E / s.N - E0),
+                       max_abs_de_i_vs_base=float((eo.cpu() - e0.repeat(n_rep)).abs().max()),
+                       max_abs_dF_vs_base=float((Fo.cpu() - F0.repeat(n_rep, 1)).abs().max()),
+                       max_abs_F=float(F0.abs().max()))
+
+    for cache in (True, False):
+        for rp in reps:
+            free_gpu()
+            print(f"# capacity: replica {rp}, layer-1 cache {cache}", file=sys.stderr, flush=True)
+            rec = {"replica": "x".join(map(str, rp)), "cache_layer1": cache}
+            try:
+                one(rp, cache, rec)
+            except torch.cuda.OutOfMemoryError as exc:
+                rec["out_of_memory"] = str(exc).splitlines()[0][:200]
+            print(json.dumps(rec), file=sys.stderr, flush=True)
+            runs.append(rec)
+    free_gpu()
+    total = torch.cuda.get_device_properties(0).total_memory / 1e9
+    out = {"capacity": "configuration-5 water box and periodic replicas, ReceiverChunkMACE E+F, chunk "
+                       f"{a.chunk or 131072}", "device_GB": round(total, 1), "runs": runs}
+    for cache in (True, False):
+        ok = sorted((r for r in runs if r["cache_layer1"] == cache and "peak_GB" in r), key=lambda r: r["atoms"])
+        if len(ok) >= 2:
+            slope = (ok[-1]["peak_GB"] - ok[0]["peak_GB"]) * 1e9 / (ok[-1]["atoms"] - ok[0]["atoms"])
+            icpt = ok[0]["peak_GB"] - slope * ok[0]["atoms"] / 1e9
+            out[f"cache_{'on' if cache else 'off'}"] = {
+                "resident_bytes_per_atom": round(slope), "fixed_GB": round(icpt, 2),
+                "largest_atoms_estimate": int((total - icpt) * 1e9 / slope), "largest_measured": ok[-1]["atoms"]}
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=None, choices=[2, 3, 4, 5],
-                    help="run one configuration only (default: configuration 5, then 3, 4 and 2 in the same run)")
+    ap.add_argument("--config", type=int, default=None, choices=[1, 2, 3, 4, 5],
+                    help="run one configuration only (default: configuration 5, then 3, 4, 2 and 1 in the same run)")
     ap.add_argument("--n-mol", type=int, default=343000, help="config 5: water molecules")
     ap.add_argument("--chunk", type=int, default=None, help="receiver chunk (default: 131072; config 3: 16384)")
     ap.add_argument("--graphs", action="store_true", default=None,
@@ -743,12 +939,18 @@ def main():
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed steps, run a plain elementwise kernel over this many MiB (reads and "
                          "writes a buffer of known size: calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--capacity", default=None, metavar="REPLICAS",
+                    help="memory and replica exactness at scale, e.g. 1x1x1,2x2x2: the configuration-5 box and its "
+                         "periodic replicas, layer-1 cache on and off; prints one JSON object and exits")
     ap.add_argument("--symc-gemm-probe", action="store_true",
                     help="time the layer-1 symmetric contraction against its dense-monomial GEMM form and exit")
     a = ap.parse_args()
     a.cpu_from = None
     if a.symc_gemm_probe:
         symc_gemm_probe()
+        return
+    if a.capacity:
+        run_capacity(a)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         exit_multi_gpu()
@@ -761,27 +963,21 @@ def main():
         line = run_md(a)
     elif cfg in (3, 4):
         line = run_ef(a)
-    else:
+    elif cfg == 2:
         line = run_conv(a)
+    else:
+        line = run_config1(a)
     if not only:
         # the other configurations in the same process, each with its own roofline and per-kernel table
         extras = {}
-        cpu5 = line.get("cpu_baseline")
-        for c, steps, warm in ((3, 20, 2), (4, 8, 1), (2, 20, 2)):
+        for c, steps, warm in ((3, 20, 2), (4, 8, 1), (2, 20, 2), (1, 20, 2)):
             free_gpu()
             print(f"# configuration {c}", file=sys.stderr, flush=True)
             b = argparse.Namespace(**vars(a))
             b.config, b.steps, b.warmup, b.chunk, b.graphs, b.copy_calib_mib = c, steps, warm, None, None, 0
-            b.no_cpu = True if c == 4 else a.no_cpu
             b.cpu_from = None
-            if c == 3 and cpu5 is not None:
-                b.cpu_from = dict(cpu5, sample="derived from configuration 5's chunk timing (same water generator, "
-                                               "density and chunk size: the same per-atom CPU work): "
-                                               + cpu5["sample"])
-            extras[f"config{c}"] = sub_line(run_ef(b) if c in (3, 4) else run_conv(b))
-            if c == 4:
-                extras["config4"]["cpu_baseline_note"] = ("not in the default run (bounded run time): "
-                                                          "bench.py --config 4 times one FCC chunk on the CPU")
+            run = {1: run_config1, 2: run_conv, 3: run_ef, 4: run_ef}[c]
+            extras[f"config{c}"] = sub_line(run(b))
         line["configs"] = extras
     print(json.dumps(line), flush=True)
 

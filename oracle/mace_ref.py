@@ -411,6 +411,61 @@ def local_graph(a, b, recv, send, loc):
     return nodes, ei_send, ei_recv, rg, sg
 
 
+def atom_energy_local(m, pos, box, spec, i, tables=None):
+    """Energy of atom i (e0 + shift + scale (R1 + R2), eV) from its own neighbourhood only: layer 1 on i and its
+    neighbours (the receivers whose h1 layer 2 of i reads), layer 2 on i.  Every atom within r_max of one of those
+    receivers is within 2 r_max of i, so only that ball of the periodic system is read; the edge vectors are the
+    fp64 minimum images x_recv - x_send and the neighbour test is the reference's dd < r_max^2, j != i
+    (receiver_chunk_mace.py:114-165).  Equal to the whole-system evaluation (three_pass, energy_full) to fp64
+    rounding, for any box larger than 2 r_max.  pos [N, 3] fp64 numpy, box [3], spec [N] element index."""
+    pos = np.asarray(pos, dtype=np.float64)
+    L = np.asarray(box, dtype=np.float64)
+    rc2 = m.r_max ** 2
+
+    def mic(v):
+        return v - L * np.round(v / L)
+
+    d = mic(pos - pos[i])
+    ball = np.nonzero((d * d).sum(1) < (2 * m.r_max + 1e-6) ** 2)[0]           # includes i
+
+    def neighbours(r):
+        v = mic(pos[r] - pos[ball])
+        keep = ((v * v).sum(1) < rc2) & (ball != r)
+        return ball[keep]
+
+    n1 = np.sort(neighbours(i))
+    recv1 = np.concatenate([[i], n1])                                          # layer-1 receivers, i first
+    loc = {int(a): k for k, a in enumerate(recv1)}
+    rg, sg = [], []
+    for r in recv1:
+        for sj in neighbours(int(r)):
+            rg.append(int(r))
+            sg.append(int(sj))
+    outside = sorted(set(sg) - set(loc))
+    for a in outside:
+        loc[a] = len(loc)
+    nodes = torch.as_tensor(np.concatenate([recv1, np.asarray(outside, dtype=np.int64)]), dtype=torch.long)
+    rg, sg = np.asarray(rg), np.asarray(sg)
+    P = torch.as_tensor(pos, dtype=F64)
+    Lt = torch.as_tensor(L, dtype=F64)
+    spec_t = torch.as_tensor(np.asarray(spec), dtype=torch.long)
+    lr = torch.as_tensor([loc[int(a)] for a in rg], dtype=torch.long)
+    ls = torch.as_tensor([loc[int(a)] for a in sg], dtype=torch.long)
+    vec1 = min_image(P[rg] - P[sg], Lt)
+    pair1 = pair2 = None
+    if tables is not None:
+        c2s = tables.col2s[spec_t]
+        pair1 = c2s[torch.as_tensor(sg)] * tables.S + c2s[torch.as_tensor(rg)]
+    with torch.no_grad():
+        h1 = layer1(m, spec_t[nodes], len(recv1), ls, lr, vec1, tables, pair1)
+        sel = lr == 0                                                          # the edges received by i
+        if tables is not None:
+            pair2 = pair1[sel]
+        e2 = layer2_energy(m, spec_t[nodes[:len(recv1)]], 1, ls[sel], lr[sel], vec1[sel], h1, tables, pair2)
+        e1 = readout1(m, h1[:1])
+    return float(m.e0[spec_t[i]] + m.shift + m.scale * (e1[0] + e2[0]))
+
+
 def three_pass(m, pos, box, spec, recv, send, chunk, tables=None):
     """ReceiverChunkMACE.compute (receiver_chunk_mace.py:278-386) in fp64: returns (E, per-atom E, F)."""
     box = torch.as_tensor(box, dtype=F64)

@@ -37,3 +37,12 @@ def water192():
     NN, rp, send = s.build_neighbors()
     recv = np.repeat(np.arange(s.N), NN)
     return dict(pos=s.pos, box=box, spec=s.spidx, recv=recv, send=send, NN=NN, raw=(pos, box, Z), sys=s)
+
+
+@pytest.fixture(scope="session")
+def water_config5():
+    """Configuration 5's water box (343,000 molecules, 1,029,000 atoms, L = 217.30 A, seed 0), host arrays
+    (pos fp64 [N, 3], box [3], Z [N]); generated once per session (about 13 s)."""
+    from mace_onegpu import systems
+    print("case config5 water box: generating 343,000 molecules", flush=True)
+    return systems.water_box(343000, seed=0)

@@ -172,15 +172,15 @@ def test_md_runner_vs_oracle(dev, scaled_model, scaled_ref, graphs):
     assert checks == 2 and md.n_rebuild >= 2
 
 
-def test_md_full_size_config5_properties(dev):
+def test_md_full_size_config5_properties(dev, water_config5):
     """Configuration 5 at full size (343,000 molecules, 1,029,000 atoms, chunk 131072): after an MD step and a
     neighbour-list rebuild, the filtered pair list equals a fresh cell-list build at r_max on the same positions
     (as sets of atom-id pairs, compared exactly), the forces sum to zero, and the energies are finite."""
     from mace_onegpu import model as mm, systems
     from mace_onegpu.md import MDRunner
     from mace_onegpu.receiver_chunk_mace import System
-    _say("case config5 full size: generating 343,000 molecules")
-    pos, box, Z = systems.water_box(343000, seed=0)
+    _say("case config5 full size")
+    pos, box, Z = water_config5
     N = len(pos)
     md = MDRunner(mm.MaceModel(seed=0), pos, box, Z, chunk=131072, device=dev)
     md.step()

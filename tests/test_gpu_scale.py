@@ -1,0 +1,78 @@
+"""Exactness at production scale (marked gpu): configuration 5's 1,029,000-atom water box evaluated by
+ReceiverChunkMACE at the production chunk of 131,072 receivers (about 11.8 M edges per chunk, 8 chunks).
+
+* Per-atom energies of 32 atoms against the fp64 oracle evaluated on each atom's own 2 r_max neighbourhood
+  (mace_ref.atom_energy_local, pinned against the whole-system oracle in tests/test_oracle.py); bar: 1e-5 eV
+  per atom (fp32 arithmetic and the 512-knot tables against the exact radial MLP).
+* The reference's replica invariance (tests/gpu/test_threepass.py:80-87) at 8.2 M atoms: the 2 x 2 x 2 periodic
+  replica (8,232,000 atoms, about 740 M pairs, 63 chunks) has the base box's energy per atom, and every atom the
+  per-atom energy and force of its base image.  The two evaluations run the same fp32 arithmetic in different
+  orders (other Morton orders, chunk boundaries and atomic-add orders), so they agree to fp32 rounding.
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+CHUNK = 131072
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _evaluate(model, pos, box, Z):
+    """(E, per-atom energies, forces) in the input atom order, on the host."""
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+    s = System(pos, box, Z - 1, 6.0, "cuda")
+    s.build_neighbors()
+    ev = ReceiverChunkMACE(model, chunk=CHUNK, device="cuda")
+    E, eat, F, PF = ev.compute(s)
+    perm = s.perm.long()
+    eo, Fo = torch.empty_like(eat), torch.empty_like(F)
+    eo[perm], Fo[perm] = eat, F
+    out = (E, eo.cpu(), Fo.cpu(), int(s.rowptr[-1]))
+    del s, ev, eat, F, PF, eo, Fo
+    torch.cuda.empty_cache()
+    return out
+
+
+@pytest.fixture(scope="module")
+def base5(model, water_config5):
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    pos, box, Z = water_config5
+    _say("case config5 base box: E+F at chunk 131072")
+    E, eat, F, n_pairs = _evaluate(model, pos, box, Z)
+    _say(f"  E/N {E / len(pos):.9f} eV, {n_pairs} pairs, max|F| {float(F.abs().max()):.4e}")
+    return E, eat, F, n_pairs
+
+
+def test_config5_per_atom_energies_vs_oracle_neighbourhoods(ref_model, water_config5, base5):
+    from oracle import mace_ref
+    pos, box, Z = water_config5
+    E, eat, F, _ = base5
+    idx = np.random.default_rng(11).choice(len(pos), 32, replace=False)
+    worst = 0.0
+    for i in idx:
+        e = mace_ref.atom_energy_local(ref_model, pos, box, Z - 1, int(i))
+        worst = max(worst, abs(float(eat[i]) - e))
+    _say(f"  32 atoms: max|e_gpu - e_oracle| {worst:.3e} eV")
+    assert worst < 1e-5
+
+
+def test_config5_replica_2x2x2_reproduces_base(model, water_config5, base5):
+    pos, box, Z = water_config5
+    E0, e0, F0, pairs0 = base5
+    N = len(pos)
+    sh = np.array([(ix, iy, iz) for ix in range(2) for iy in range(2) for iz in range(2)], dtype=np.float64)
+    pos_r = (pos[None] + (sh * box)[:, None, :]).reshape(-1, 3)
+    _say(f"case config5 replica 2x2x2: {len(pos_r)} atoms")
+    E, eat, F, n_pairs = _evaluate(model, pos_r, 2 * np.asarray(box), np.tile(Z, 8))
+    dE = abs(E / len(pos_r) - E0 / N)
+    de = float((eat - e0.repeat(8)).abs().max())
+    dF = float((F - F0.repeat(8, 1)).abs().max())
+    Fm = float(F0.abs().max())
+    _say(f"  {n_pairs} pairs; |dE/N| {dE:.3e} eV, max|de_i| {de:.3e} eV, max|dF| {dF:.3e} eV/A (max|F| {Fm:.3e})")
+    assert n_pairs == 8 * pairs0
+    assert dE < 1e-9 and de < 1e-6 and dF < 1e-5 * Fm

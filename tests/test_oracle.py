@@ -129,3 +129,20 @@ def test_tables_converge_to_the_mlp(ref_model, water192):
         errs.append(float((Ft - F).abs().max()))
     assert errs[1] < 1e-4 * float(F.abs().max())
     assert errs[1] < errs[0] / 4                    # cubic convergence (factor ~8 per halving of h)
+
+
+def test_atom_energy_local_matches_whole_system(ref_model, water192):
+    """The per-atom energy evaluated from the atom's own 2 r_max neighbourhood (the production-scale spot check's
+    oracle) equals the whole-system three-pass per-atom energy (fp64 rounding), for O and H atoms of the periodic
+    192-atom box; with the 512-knot tables as well."""
+    w = water192
+    E3, eat, F3, _, _ = mace_ref.three_pass(ref_model, w["pos"], w["box"], w["spec"], w["recv"], w["send"], chunk=192)
+    for i in (0, 1, 2, 97, 191):
+        e = mace_ref.atom_energy_local(ref_model, w["pos"], w["box"], w["spec"], i)
+        assert abs(e - float(eat[i])) < 1e-12 * max(1.0, abs(e)), (i, e, float(eat[i]))
+    tab = mace_ref.Tables64(ref_model, sorted(set(np.asarray(w["spec"]).tolist())), n_grid=512)
+    E3t, eat_t, _, _, _ = mace_ref.three_pass(ref_model, w["pos"], w["box"], w["spec"], w["recv"], w["send"],
+                                              chunk=96, tables=tab)
+    for i in (4, 150):
+        e = mace_ref.atom_energy_local(ref_model, w["pos"], w["box"], w["spec"], i, tables=tab)
+        assert abs(e - float(eat_t[i])) < 1e-12 * max(1.0, abs(e))
