@@ -185,14 +185,17 @@ class FastLayers:
         self.M, self.r_lo, self.r_hi = int(spline_grid), float(r_lo), sp.r_max
         self.h = (self.r_hi - self.r_lo) / (self.M - 1)
         self.inv_h = 1.0 / self.h
-        # the radial embedding of this architecture has no species-dependent distance transform: every ordered
-        # pair has the same W(r), so one table serves all pairs (pair_map -> 0)
-        self.n_tab = 1
-        self.pair_map = torch.zeros(S * S, dtype=torch.int32, device=dev)
+        # one spline table per distinct radial network of the ordered pairs (sender s outer, receiver r inner):
+        # pair_map[s * S + r] -> table.  This architecture has one network per block (every pair -> table 0); a
+        # model with per-pair networks (model.pair_radial) gets one table per distinct network
+        self.radial_sets, pm = self._pair_radial_sets(model, P)
+        self.n_tab = len(self.radial_sets)
+        self.pair_map = torch.tensor(pm, dtype=torch.int32, device=dev)
         self.tab = [self._build_table(P, k) for k in range(2)]
         # -------- layer 1 in the exact density-projection (ACE) form: per-edge ht x Y outer products on MFMA,
-        # one GEMM per atom with the folded weights G[l, s_recv] (up to 4 species)
-        self.ace = bool(ace_layer1) and S <= ACE_MAX_S
+        # one GEMM per atom with the folded weights G[l, s_recv] (up to 4 species).  It factors W = ht(r) A3 with
+        # one ht for all pairs, so per-pair networks take the spline-convolution path
+        self.ace = bool(ace_layer1) and S <= ACE_MAX_S and self.n_tab == 1
         if self.ace:
             self._build_ace(P, comb)
         # -------- linear plans
@@ -241,21 +244,43 @@ class FastLayers:
         self.ktimer.append((name, units, e0, e1))
 
     # ------------------------------------------------------------------ tables
+    def _pair_radial_sets(self, model, P):
+        """Distinct radial networks of the ordered species pairs of this system and the pair -> table map: a list
+        of {k: [r0..r3] fp64} (table order) and pair_map[s * S + r] (s sender, r receiver; the reference's ordered
+        pair index, spline_w.py:18-27)."""
+        default = {k: [P[f"i{k}_r{j}"] for j in range(4)] for k in range(2)}
+        pr = getattr(model, "pair_radial", None)
+        sets, pm = [], []
+        for a in self.cols:
+            for b in self.cols:
+                d = pr.get((a, b)) if pr is not None else None
+                ws = {k: [w.detach().to("cpu", torch.float64) for w in d[k]] if d is not None and k in d
+                      else default[k] for k in range(2)}
+                for t, other in enumerate(sets):
+                    if all(torch.equal(x, y) for k in range(2) for x, y in zip(ws[k], other[k])):
+                        pm.append(t)
+                        break
+                else:
+                    pm.append(len(sets))
+                    sets.append(ws)
+        return sets, pm
+
     def _build_table(self, P, k):
-        """conv_spline.build_tables / spline_radial._sample on the GPU in fp64, then per-interval coefficients."""
+        """conv_spline.build_tables / spline_radial._sample on the GPU in fp64, then per-interval coefficients, one
+        table per distinct radial network (self.radial_sets)."""
         dev = self.dev
-        Ws = [P[f"i{k}_r{j}"].to(dev).contiguous() for j in range(4)]
         nW = self.tables.tp1["nW"] if k == 0 else self.tables.tp2["nW"]
         D = nW * C
         M = self.M
         r = torch.linspace(self.r_lo, self.r_hi, M, dtype=torch.float64, device=dev)
         eps = 1e-5 * (self.r_hi - self.r_lo)
         pts = torch.cat([r, r + eps, r - eps]).contiguous()
-        samples = torch.empty(3 * M, D, dtype=torch.float64, device=dev)
-        K.mm_radial_mlp_f64(3 * M, pts, Ws[0], Ws[1], Ws[2], Ws[3], self.spec.num_bessel, Ws[1].shape[0], D,
-                            self.spec.r_max, self.spec.p_cutoff, mm.SILU_NORM, samples, stream())
         coef = torch.empty(NCB * self.n_tab * (M - 1) * nW * 16 * 4, dtype=torch.float32, device=dev)
-        for tb in range(self.n_tab):
+        for tb, ws in enumerate(self.radial_sets):
+            Ws = [w.to(dev).contiguous() for w in ws[k]]
+            samples = torch.empty(3 * M, D, dtype=torch.float64, device=dev)
+            K.mm_radial_mlp_f64(3 * M, pts, Ws[0], Ws[1], Ws[2], Ws[3], self.spec.num_bessel, Ws[1].shape[0], D,
+                                self.spec.r_max, self.spec.p_cutoff, mm.SILU_NORM, samples, stream())
             K.mm_spline_coeffs(samples, M, nW, eps, self.h, tb, self.n_tab, coef, stream())
         return coef
 

@@ -139,6 +139,12 @@ class MaceModel(torch.nn.Module):
             v.data = v.data.float().double()
         self.p = torch.nn.ParameterDict(p)
         self.register_buffer("e0", torch.zeros(ne, dtype=torch.float64))
+        # radial networks per ordered element pair: {(sender column, receiver column): {block k: [r0, .., r3]}}
+        # for models whose radial weights depend on the species pair (MACE-MPA-0's species-pair distance transform
+        # makes W(r) a different function for every ordered pair); pairs not listed use i{k}_r*.  None: one
+        # network per block for all pairs (this architecture).  The kernels then read one spline table per
+        # distinct network (FastLayers).
+        self.pair_radial = None
         self.to(dtype)
 
     # -- attributes the ML-IAP wrapper reads from a mace model

@@ -225,6 +225,12 @@ class RefModel:
         self.tp1, self.tp2, self.sc1, self.sc2, self.lin2_src = t.tp1, t.tp2, t.sc1, t.sc2, t.lin2_src
         self.coupling = coupling
         self.nlayers_r = len(sp.radial_mlp) + 1
+        # optional radial networks per ordered element pair (sender column, receiver column) -> {block k: weight
+        # list}; pairs not listed use the model's own networks (mace_onegpu.model.MaceModel.pair_radial)
+        pr = getattr(model, "pair_radial", None)
+        self.pair_radial = None if pr is None else {
+            (int(a), int(b)): {k: [w.detach().to("cpu", F64) for w in ws] for k, ws in d.items()}
+            for (a, b), d in pr.items()}
 
     def astype(self, dtype):
         """A copy whose parameters are held in `dtype` (the fp32 CPU baseline evaluates the same functions)."""
@@ -234,7 +240,12 @@ class RefModel:
         m.e0 = self.e0.to(dtype)
         return m
 
-    def radial_W(self, k):
+    def radial_W(self, k, send_col=None, recv_col=None):
+        """Radial-network weights of block k; with element columns, those of the ordered pair (sender, receiver)."""
+        if self.pair_radial is not None and send_col is not None:
+            d = self.pair_radial.get((int(send_col), int(recv_col)))
+            if d is not None and k in d:
+                return d[k]
         return [self.P[f"i{k}_r{j}"] for j in range(self.nlayers_r)]
 
     def sym_weights(self, k, Ls):
@@ -258,16 +269,20 @@ class Tables64:
         eps = 1e-5 * (self.r_hi - r_lo)
         self.TV, self.TG = [], []
         for k in range(2):
-            Ws = m.radial_W(k)
+            tv, tg = [], []
+            # ordered pairs p = a * S + b, sender species a outer, receiver b inner (spline_radial._sample,
+            # spline_radial.py:121-151); without per-pair networks every pair holds the same function
+            for a in range(S):
+                for b in range(S):
+                    Ws = m.radial_W(k, species_cols[a], species_cols[b])
 
-            def f(rr):
-                return radial_mlp(bessel(rr, m.r_max, m.nb), Ws) * poly_cutoff(rr, m.r_max, m.p)[:, None]
-            v0, vp, vm = f(r), f(r + eps), f(r - eps)
-            d = (vp - vm) / (2 * eps)
-            # ordered pairs (sender a outer, receiver b inner); the radial embedding of this model does not
-            # depend on the species, so every pair holds the same function
-            self.TV.append(torch.cat([v0] * (S * S), 0))           # [P*M, D]
-            self.TG.append(torch.cat([d * self.h] * (S * S), 0))
+                    def f(rr):
+                        return radial_mlp(bessel(rr, m.r_max, m.nb), Ws) * poly_cutoff(rr, m.r_max, m.p)[:, None]
+                    v0, vp, vm = f(r), f(r + eps), f(r - eps)
+                    tv.append(v0)
+                    tg.append((vp - vm) / (2 * eps) * self.h)
+            self.TV.append(torch.cat(tv, 0))                       # [P*M, D]
+            self.TG.append(torch.cat(tg, 0))
 
     def astype(self, dtype):
         import copy
@@ -297,11 +312,24 @@ def _edge(m, vec):
     return r, Y, B, f
 
 
-def _weights_density(m, k, r, B, f, tables, pair):
-    if tables is None:
+def _weights_density(m, k, r, B, f, tables, pair, cs=None, cr=None):
+    """Radial weights W [E, nW C] (table lookup, or the radial network of each edge's ordered element pair
+    (cs[e], cr[e]) = (sender, receiver) column) and the edge density."""
+    if tables is not None:
+        W = tables.lookup(k, r, pair)
+    elif m.pair_radial is None:
         W = radial_mlp(B, m.radial_W(k)) * f[:, None]
     else:
-        W = tables.lookup(k, r, pair)
+        code = cs * m.ne + cr
+        W = None
+        for c in torch.unique(code).tolist():
+            sel = code == c
+            w = radial_mlp(B[sel], m.radial_W(k, c // m.ne, c % m.ne)) * f[sel][:, None]
+            if W is None:
+                W = torch.zeros(B.shape[0], w.shape[1], dtype=w.dtype)
+            W = W.index_put((torch.nonzero(sel).squeeze(1),), w)
+        if W is None:
+            W = torch.zeros(0, m.P[f"i{k}_r{m.nlayers_r - 1}"].shape[1], dtype=B.dtype)
     return W, edge_density(B, m.P[f"i{k}_dens"], f)
 
 
@@ -310,7 +338,7 @@ def layer1_message(m, spec_nodes, nC, send, recv, vec, tables=None, pair=None):
     before skip_tp: linear(sum_e TP(W_e, X[send_e], Y_e)) / (rho + 1) [nC, 16, C], rho = sum_e d_e."""
     C = m.C
     r, Y, B, f = _edge(m, vec)
-    W, d = _weights_density(m, 0, r, B, f, tables, pair)
+    W, d = _weights_density(m, 0, r, B, f, tables, pair, spec_nodes[send], spec_nodes[recv])
     W = W.reshape(-1, m.tp1["nW"], C)
     onehot = torch.nn.functional.one_hot(spec_nodes, m.ne).to(m.P["emb"].dtype)
     X = per_l_linear(node_embedding(onehot, m.P["emb"])[:, None, :], [0], m.P["i0_up"], C)
@@ -342,7 +370,7 @@ def layer2_energy(m, spec_nodes, nC, send, recv, vec, h1_nodes, tables=None, pai
     sc = skip_tp(h1_nodes[:nC, 0:1, :], s, m.P["i1_skip"])[:, 0, :]
     X = per_l_linear(h1_nodes, [0, 1], m.P["i1_up"], C)
     r, Y, B, f = _edge(m, vec)
-    W, d = _weights_density(m, 1, r, B, f, tables, pair)
+    W, d = _weights_density(m, 1, r, B, f, tables, pair, spec_nodes[send], spec_nodes[recv])
     W = W.reshape(-1, m.tp2["nW"], C)
     mji = channelwise_tp(W, X, Y, send, m.tp2["paths"], m.tp2["in_ls"], m.coupling)
     A = scatter_sum(mji, recv, nC)

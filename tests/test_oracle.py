@@ -146,3 +146,61 @@ def test_atom_energy_local_matches_whole_system(ref_model, water192):
     for i in (4, 150):
         e = mace_ref.atom_energy_local(ref_model, w["pos"], w["box"], w["spec"], i, tables=tab)
         assert abs(e - float(eat_t[i])) < 1e-12 * max(1.0, abs(e))
+
+
+def _pair_networks(model, seed, pairs):
+    """Random radial networks (fp32-representable fp64 values, the model's layer sizes) for the given ordered
+    (sender column, receiver column) pairs: {pair: {block k: [r0..r3]}}; pairs listed together share one network."""
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for group in pairs:
+        nets = {k: [torch.randn(*model.p[f"i{k}_r{j}"].shape, generator=g, dtype=torch.float64).float().double()
+                    for j in range(4)] for k in range(2)}
+        for pr in group:
+            out[pr] = nets
+    return out
+
+
+@pytest.fixture(scope="module")
+def pair_model():
+    """The seed-0 model with a radial network per ordered pair of H (column 0) and O (column 7): (H, H) and
+    (O, O) share one, (H, O) and (O, H) (sender, receiver) have their own."""
+    from mace_onegpu import model as mm
+    m = mm.MaceModel(seed=0)
+    m.pair_radial = _pair_networks(m, 5, [[(0, 0), (7, 7)], [(0, 7)], [(7, 0)]])
+    return m
+
+
+def test_pair_networks_equal_to_the_default_reproduce_it(model, ref_model, water192):
+    """Per-pair networks that are all the model's own network: the per-edge selection gives the default result."""
+    from mace_onegpu import model as mm, o3
+    w = water192
+    m = mm.MaceModel(seed=0)
+    own = {k: [model.p[f"i{k}_r{j}"].detach().double() for j in range(4)] for k in range(2)}
+    m.pair_radial = {(a, b): own for a in (0, 7) for b in (0, 7)}
+    rm = mace_ref.RefModel(m, o3.coupling)
+    E0, e0, F0 = mace_ref.energy_forces_full(ref_model, w["pos"], w["box"], w["spec"], w["recv"], w["send"])
+    E1, e1, F1 = mace_ref.energy_forces_full(rm, w["pos"], w["box"], w["spec"], w["recv"], w["send"])
+    assert abs(E1 - E0) < 1e-12 * abs(E0) + 1e-12 and float((F1 - F0).abs().max()) < 1e-12
+
+
+def test_pair_tables_follow_the_per_edge_networks(pair_model, water192):
+    """Three-pass with the per-pair 512-knot tables (ordered pair p = s_send S + s_recv) against the full graph with
+    each edge's own (sender, receiver) network: equal to the tables' interpolation error.  Swapping the (H, O) and
+    (O, H) networks changes the result by far more, so a transposed pair index would fail."""
+    from mace_onegpu import o3
+    w = water192
+    rm = mace_ref.RefModel(pair_model, o3.coupling)
+    E, e, F = mace_ref.energy_forces_full(rm, w["pos"], w["box"], w["spec"], w["recv"], w["send"])
+    tab = mace_ref.Tables64(rm, [0, 7], n_grid=512)
+    Et, et, Ft, _, _ = mace_ref.three_pass(rm, w["pos"], w["box"], w["spec"], w["recv"], w["send"], chunk=96,
+                                           tables=tab)
+    N = len(w["pos"])
+    dF = float((Ft - F).abs().max())
+    assert abs(Et - E) / N < 1e-6 and dF < 1e-4 * float(F.abs().max())
+    swapped = dict(rm.pair_radial)
+    swapped[(0, 7)], swapped[(7, 0)] = rm.pair_radial[(7, 0)], rm.pair_radial[(0, 7)]
+    rs = mace_ref.RefModel(pair_model, o3.coupling)
+    rs.pair_radial = swapped
+    Es, es, Fs = mace_ref.energy_forces_full(rs, w["pos"], w["box"], w["spec"], w["recv"], w["send"])
+    assert float((Fs - F).abs().max()) > 100 * dF and abs(Es - E) / N > 100 * abs(Et - E) / N
