@@ -853,13 +853,14 @@ def replicate(pos, box, Z, reps):
 
 
 def run_capacity(a):
-    """Memory and exactness at scale: the configuration-5 water box and its periodic replicas evaluated with
-    ReceiverChunkMACE (chunk 131072, eager chunks) with the pass-A layer-1 cache on and off.  Per run: peak device
-    GB (torch allocator), seconds per E+F, E/N and, for replicas, the largest deviations of per-atom energies and
-    forces from the base box's (atom j of a replica is atom j % N of the base).  resident bytes per atom = the slope
-    of peak GB against N between the base and the largest replica; the largest N on this GPU follows from that
-    line and the device's memory (what torch may allocate)."""
-    import numpy as np
+    """Memory and exactness at scale: the configuration-5 water box and its periodic replicas evaluated by
+    ReceiverChunkMACE (chunk 131072, eager chunks) in three memory layouts: the default one with the pass-A
+    layer-1 cache, without it, and low_memory (chunk topologies per pass, per-chunk force sums: the reference's
+    layout).  Per run: peak device GB (torch allocator), seconds per E+F, E/N and, for replicas, the largest
+    deviations of per-atom energies and forces from the base box's (atom j of a replica is atom j % N of the base).
+    resident bytes per atom = the slope of peak GB against N between the base and the largest replica that fits;
+    the largest N on this GPU follows from that line and the device's memory.  A layout is not tried on replicas
+    larger than one it ran out of memory on."""
     import torch
 
     from mace_onegpu import model as mm, systems
@@ -867,15 +868,17 @@ def run_capacity(a):
     pos, box, Z = systems.water_box(a.n_mol, seed=0)
     model = mm.MaceModel(seed=0)
     reps = [tuple(int(x) for x in r.split("x")) for r in a.capacity.split(",")]
+    modes = {"cache_on": dict(cache_layer1=True), "cache_off": dict(cache_layer1=False),
+             "low_memory": dict(low_memory=True)}
     runs, base = [], {}
 
-    def one(rp, cache, rec):
+    def one(rp, mode, rec):
         n_rep = rp[0] * rp[1] * rp[2]
         p_r, b_r, z_r = replicate(pos, box, Z, rp) if n_rep > 1 else (pos, box, Z)
         rec["atoms"] = len(p_r)
         s = System(p_r, b_r, z_r - 1, 6.0, "cuda")
         s.build_neighbors()
-        ev = ReceiverChunkMACE(model, chunk=a.chunk or 131072, device="cuda", cache_layer1=cache)
+        ev = ReceiverChunkMACE(model, chunk=a.chunk or 131072, device="cuda", **modes[mode])
         ev.compute(s)                  # set-up call (tables, workspaces)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -889,37 +892,39 @@ def run_capacity(a):
         eo = torch.empty_like(eat)
         eo[perm] = eat
         if n_rep == 1:
-            base[cache] = (E / s.N, Fo.cpu(), eo.cpu())
-        elif cache in base:
-            E0, F0, e0 = base[cache]
+            base[mode] = (E / s.N, Fo.cpu(), eo.cpu())
+        elif mode in base:
+            E0, F0, e0 = base[mode]
             rec.update(dE_per_atom_vs_base=abs(E / s.N - E0),
                        max_abs_de_i_vs_base=float((eo.cpu() - e0.repeat(n_rep)).abs().max()),
                        max_abs_dF_vs_base=float((Fo.cpu() - F0.repeat(n_rep, 1)).abs().max()),
                        max_abs_F=float(F0.abs().max()))
 
-    for cache in (True, False):
+    for mode in modes:
         for rp in reps:
             free_gpu()
-            print(f"# capacity: replica {rp}, layer-1 cache {cache}", file=sys.stderr, flush=True)
-            rec = {"replica": "x".join(map(str, rp)), "cache_layer1": cache}
+            print(f"# capacity: replica {rp}, {mode}", file=sys.stderr, flush=True)
+            rec = {"replica": "x".join(map(str, rp)), "layout": mode}
             try:
-                one(rp, cache, rec)
+                one(rp, mode, rec)
             except torch.cuda.OutOfMemoryError as exc:
                 rec["out_of_memory"] = str(exc).splitlines()[0][:200]
             print(json.dumps(rec), file=sys.stderr, flush=True)
             runs.append(rec)
+            if "out_of_memory" in rec:
+                break
     free_gpu()
     total = torch.cuda.get_device_properties(0).total_memory / 1e9
     out = {"capacity": "configuration-5 water box and periodic replicas, ReceiverChunkMACE E+F, chunk "
                        f"{a.chunk or 131072}", "device_GB": round(total, 1), "runs": runs}
-    for cache in (True, False):
-        ok = sorted((r for r in runs if r["cache_layer1"] == cache and "peak_GB" in r), key=lambda r: r["atoms"])
+    for mode in modes:
+        ok = sorted((r for r in runs if r["layout"] == mode and "peak_GB" in r), key=lambda r: r["atoms"])
         if len(ok) >= 2:
             slope = (ok[-1]["peak_GB"] - ok[0]["peak_GB"]) * 1e9 / (ok[-1]["atoms"] - ok[0]["atoms"])
             icpt = ok[0]["peak_GB"] - slope * ok[0]["atoms"] / 1e9
-            out[f"cache_{'on' if cache else 'off'}"] = {
-                "resident_bytes_per_atom": round(slope), "fixed_GB": round(icpt, 2),
-                "largest_atoms_estimate": int((total - icpt) * 1e9 / slope), "largest_measured": ok[-1]["atoms"]}
+            out[mode] = {"resident_bytes_per_atom": round(slope), "fixed_GB": round(icpt, 2),
+                         "largest_atoms_estimate": int((total - icpt) * 1e9 / slope),
+                         "largest_measured": ok[-1]["atoms"]}
     print(json.dumps(out), flush=True)
 
 

@@ -209,6 +209,12 @@ int mm_gather_rows_csr(const int* rowptr, const int* idx, const float* src, long
 /* per-atom forces from pair forces (ReceiverChunkMACE._accum_forces, receiver_chunk_mace.py:272-276) */
 int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* send_rowptr, const long* send_perm,
                             const float* pair_force, double* F, mm_stream_t stream);
+/* per-chunk force accumulation of the low-memory evaluator (ReceiverChunkMACE._accum_forces,
+ * receiver_chunk_mace.py:272-276): F[nodes[n]] += -(sum of the chunk's pair forces received by node n < nC)
+ * + (sum of those it sends, through the chunk's sender CSR s_rowptr [n_nodes + 1] / s_perm [nE] of chunk-local
+ * edge ids); pf [nE, 3] holds only this chunk's pair forces.  Deterministic (fixed per-node order). */
+int mm_chunk_forces(int n_nodes, int nC, const int* rowptr, const int* s_rowptr, const int* s_perm, const int* nodes,
+                    const float* pair_force, double* F, mm_stream_t stream);
 /* the same per-atom forces for an MD step whose pair list was filtered from a skin list: through the skin list's
  * reverse-pair map (rev) and the filter's index map, without sorting the pairs by sender (no counterpart in the
  * reference, whose MD runs inside LAMMPS) */

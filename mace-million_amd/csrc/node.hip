@@ -319,6 +319,59 @@ extern "C" int mm_pair_forces_to_atoms(int n, const long* rowptr, const long* s_
   return mm::launch_status("mm_pair_forces_to_atoms");
 }
 
+// Per-chunk force accumulation of the low-memory evaluator (the reference's ReceiverChunkMACE._accum_forces,
+// receiver_chunk_mace.py:272-276, which index_adds each chunk's edge gradients into F): for every node n of the
+// chunk, F[nodes[n]] += -(sum of PF over the edges received by n, when n < nC is a receiver) + (sum of PF over the
+// edges sent by n, through the chunk's sender CSR).  Only this chunk's pair forces (pf [nE, 3], chunk-local edge
+// order) are read, so no pair-force array of the whole system is kept.  One wave per node, the lanes striding
+// over its edges, fp64 sums and a fixed xor butterfly: the result does not depend on scheduling, and chunks are
+// added in the order the host launches them.
+__global__ void __launch_bounds__(256) mm_chunk_forces_kernel(int n_nodes, int nC, const int* __restrict__ rowptr,
+                                                              const int* __restrict__ s_rowptr,
+                                                              const int* __restrict__ s_perm,
+                                                              const int* __restrict__ nodes,
+                                                              const float* __restrict__ pf, double* __restrict__ F) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= n_nodes) return;
+  const int lane = threadIdx.x & 63;
+  double fx = 0, fy = 0, fz = 0;
+  if (n < nC) {
+    const int r1 = rowptr[n + 1];
+    for (int e = rowptr[n] + lane; e < r1; e += 64) {
+      fx -= pf[3L * e];
+      fy -= pf[3L * e + 1];
+      fz -= pf[3L * e + 2];
+    }
+  }
+  const int s1 = s_rowptr[n + 1];
+  for (int k = s_rowptr[n] + lane; k < s1; k += 64) {
+    const long e = s_perm[k];
+    fx += pf[3 * e];
+    fy += pf[3 * e + 1];
+    fz += pf[3 * e + 2];
+  }
+  for (int o = 32; o >= 1; o >>= 1) {
+    fx += __shfl_xor(fx, o);
+    fy += __shfl_xor(fy, o);
+    fz += __shfl_xor(fz, o);
+  }
+  if (lane == 0) {
+    const long i = nodes[n];
+    F[3 * i] += fx;
+    F[3 * i + 1] += fy;
+    F[3 * i + 2] += fz;
+  }
+}
+
+extern "C" int mm_chunk_forces(int n_nodes, int nC, const int* rowptr, const int* s_rowptr, const int* s_perm,
+                               const int* nodes, const float* pf, double* F, hipStream_t stream) {
+  MM_CHECK_ARG(n_nodes >= 0 && nC >= 0 && nC <= n_nodes, "bad sizes (0 <= nC <= n_nodes)");
+  if (n_nodes == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_chunk_forces_kernel, dim3((unsigned)((n_nodes + 3L) / 4)), dim3(256), 0, stream, n_nodes, nC,
+                     rowptr, s_rowptr, s_perm, nodes, pf, F);
+  return mm::launch_status("mm_chunk_forces");
+}
+
 // Per-atom forces of an MD step from the pair forces of the filtered list, through the skin list (no sort): for
 // every skin pair e of atom i that survived the filter (fidx[e] = its index in the filtered list, -1 otherwise),
 // F[i] += -PF[fidx[e]] + PF[fidx[rev[e]]], rev[e] = the skin index of the reverse pair (j, i); the neighbour test

@@ -72,6 +72,7 @@ SIGNATURES = {
     "mm_ghost_reverse": [P, P, I, I, P, P, P],
     "mm_pair_forces_to_atoms": [I, P, P, P, P, P, P],
     "mm_pair_forces_skin": [L, P, P, P, P, P, P],
+    "mm_chunk_forces": [I, I, P, P, P, P, P, P, P],
     "mm_chunk_edge_index": [L, P, P, P, I, P, P, P],
     # tables
     "mm_radial_mlp_f64": [I, P, P, P, P, P, I, I, I, D, I, D, P, P],

@@ -437,10 +437,25 @@ class FastLayers:
         else:
             self._layer1_forward(g, H1[g.a:g.b], cache["M"][g.a:g.b], cache["rho"][g.a:g.b])
 
-    def pass_c(self, g, G1r, PF, eat, H1=None, cache=None):
+    def _chunk_pair_forces(self, g, PF, forces):
+        """Where the chunk's pair forces go: PF[e0:e1] of the whole system, or (forces = per-atom F, fp64 [N, 3])
+        the chunk's own buffer, added to F by mm_chunk_forces after the pass."""
+        if forces is None:
+            return PF[g.e0:g.e1]
+        ws = self.ws
+        if ws.get("pf") is None or ws["pf"].shape[0] < ws["E"]:
+            ws["pf"] = torch.empty(ws["E"], 3, dtype=torch.float32, device=self.dev)
+        return ws["pf"][:g.nE]
+
+    def _add_chunk_forces(self, g, pf, forces):
+        srp, sperm = sender_csr(g)
+        K.mm_chunk_forces(g.n_nodes, g.nC, g.rowptr, srp, sperm, g.nodes, pf, forces, stream())
+
+    def pass_c(self, g, G1r, PF, eat, H1=None, cache=None, forces=None):
         """Layer 1 with gradient: eat[a:b] += scale R1(h1); PF[e0:e1] += d(scale R1 + G1r . h1)/dv
         (mliap_threepass.py:564-582).  With the pass-A cache (and H1), the layer-1 forward is not recomputed: the
-        stored message, density and h1 are exactly what the recomputation would produce."""
+        stored message, density and h1 are exactly what the recomputation would produce.  With forces (per-atom
+        F, fp64 [N, 3]) the chunk's pair forces are added to F instead (PF unused)."""
         ws = self.prepare(g)
         if cache is None:
             h1, Mc, rho = ws["h"], ws["M"], ws["rho"]
@@ -468,13 +483,17 @@ class FastLayers:
                         ws["e_u"], self.Xs1, C, self.tab[0], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
                         ws["E"] * 17, None, stream())
             n_part = NCB
+        pf = self._chunk_pair_forces(g, PF, forces)
         K.mm_edge_grad(g.nE, g.E_dev, ws["part"], ws["E"] * 17, n_part, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
-                       PF[g.e0:g.e1], 1, stream())
+                       pf, 0 if forces is not None else 1, stream())
+        if forces is not None:
+            self._add_chunk_forces(g, pf, forces)
 
     # ------------------------------------------------------------------ layer 2
-    def pass_b(self, g, H1x, G1, PF, eat):
+    def pass_b(self, g, H1x, G1, PF, eat, forces=None):
         """Layer-2 energy with gradient: eat[a:b] += scale R2(h2); PF[e0:e1] = dE2/dv; G1[nodes] += dE2/dh1
-        (mliap_threepass.py:531-553)."""
+        (mliap_threepass.py:531-553).  With forces (per-atom F, fp64 [N, 3]) the chunk's pair forces are added to
+        F instead (PF unused)."""
         ws = self.prepare(g)
         D1 = 4 * C
         h2, gh2, B2, gB2 = ws["h"], ws["gh"], ws["B"], ws["gB"]       # [nC, 128] views of the wider buffers
@@ -509,8 +528,11 @@ class FastLayers:
             self._timed("conv2_bwd", (g.nE, g.nC, g.n_nodes), K.mm_conv2_bwd, g.rowptr, g.nC, ws["e_pk"], ws["e_u"],
                         ws["Xh"], D1, self.tab[1], self.n_tab, self.M, self.inv_h, ws["gA"], ws["part"],
                         ws["E"] * 17, ws["gXh"], stream())
+        pf = self._chunk_pair_forces(g, PF, forces)
         K.mm_edge_grad(g.nE, g.E_dev, ws["part"], ws["E"] * 17, NCB, ws["g_rho"], ws["e_recv"], ws["e_dd"], ws["e_u"],
-                       PF[g.e0:g.e1], 0, stream())
+                       pf, 0, stream())
+        if forces is not None:
+            self._add_chunk_forces(g, pf, forces)
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1,
                   count_dev=g.N_dev)
         self._lin(self.plan_sk1, gh2, C, G1, D1, self.W_sk1T, g.nC, out_rows=g.nodes, species=True, w_group_stride=1,

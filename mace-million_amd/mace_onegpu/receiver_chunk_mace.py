@@ -179,8 +179,15 @@ class ReceiverChunkMACE:
     """Three-pass energy + forces of a System with the MI355X kernels (fp32 arithmetic, fp64 energies and forces)."""
 
     def __init__(self, model, chunk=16384, spline_grid=512, device="cuda", cache_layer1=True, use_graphs=False,
-                 e_align=65536, ace_layer1=True, check=None, deterministic=None):
+                 e_align=65536, ace_layer1=True, check=None, deterministic=None, low_memory=False):
         self.model, self.chunk, self.spline_grid = model, int(chunk), int(spline_grid)
+        # low_memory: the reference's own memory layout (receiver_chunk_mace.py:278-386): each chunk's topology is
+        # built when a pass reaches it and dropped after it, and each chunk's pair forces are added to F at once
+        # (mm_chunk_forces), so what stays resident per atom is the positions, the pair list, H1, G1 and F.  No
+        # HIP graphs and no layer-1 cache in this mode; compute() returns PF = None.
+        self.low_memory = bool(low_memory)
+        if self.low_memory and use_graphs:
+            raise ValueError("low_memory evaluates chunks eagerly (no HIP graphs)")
         # host-side range check of every chunk's index arrays before its kernels run (check_chunk)
         self.check = (os.environ.get("MACE3P_CHECK", "0") == "1") if check is None else bool(check)
         # bitwise-repeatable evaluations (the sender-feature gradient summed in a fixed order, FastLayers)
@@ -191,7 +198,7 @@ class ReceiverChunkMACE:
         self.fl = None
         self.D1 = 4 * model.spec.C
         # keep pass A's layer-1 message and density (8 KiB per atom) so that pass C does not recompute them
-        self.cache_layer1 = bool(cache_layer1)
+        self.cache_layer1 = bool(cache_layer1) and not self.low_memory
         self._cache = None
         # full chunks replayed from HIP graphs (chunk_graphs.ChunkGraphExec), recaptured when a capacity is exceeded
         self.use_graphs, self.e_align = bool(use_graphs), int(e_align)
@@ -216,24 +223,26 @@ class ReceiverChunkMACE:
         fl = self._layers(sysm)
         if getattr(sysm, "chunk_graphs", None) is not None:
             return sysm.chunk_graphs(self.chunk, fl.col2s)
+        return list(self._chunk_iter(sysm, fl))
+
+    def _chunk_iter(self, sysm, fl, rp_cpu=None):
+        """The chunks of a System one at a time (topology built when the chunk is reached)."""
         dev, N = self.dev, sysm.N
         rp = sysm.rowptr
-        rp_cpu = rp.cpu().numpy()
-        recv_all = torch.repeat_interleave(torch.arange(N, device=dev, dtype=torch.int32), sysm.NN.long())
+        rp_cpu = rp.cpu().numpy() if rp_cpu is None else rp_cpu
         loc = torch.full((N,), -1, dtype=torch.int32, device=dev)
         flag = torch.zeros(N, dtype=torch.bool, device=dev)
         node_spec_all = fl.col2s[sysm.spidx.long()]
         box_h = host_f64(sysm.box)
-        out = []
         for a in range(0, N, self.chunk):
             b = min(a + self.chunk, N)
             e0, e1 = int(rp_cpu[a]), int(rp_cpu[b])
             nodes, ls = chunk_topology(a, b, e0, e1, sysm.send, loc, flag)
             g = make_chunk(a, b, e0, e1, nodes, ls, rp, node_spec_all)
             g.pos, g.box_host = sysm.pos, box_h
-            g.recv_local = (recv_all[e0:e1] - a).contiguous()
-            out.append(g)
-        return out
+            g.recv_local = torch.repeat_interleave(torch.arange(b - a, device=dev, dtype=torch.int32),
+                                                   sysm.NN[a:b].long(), output_size=e1 - e0)
+            yield g
 
     def _checked(self, graphs, sysm, fl):
         if self.check:
@@ -265,8 +274,49 @@ class ReceiverChunkMACE:
         gx.begin(graphs)
         return gx
 
+    def _compute_low_memory(self, sysm, timings):
+        """The three passes with each chunk's topology rebuilt when a pass reaches it and its pair forces added to
+        F at once (low_memory); returns (E, eat, F, None)."""
+        fl = self._layers(sysm)
+        dev, N = self.dev, sysm.N
+        rp_cpu = sysm.rowptr.cpu().numpy()
+        sync = torch.cuda.synchronize if timings is not None else (lambda: None)
+        t, t0 = {}, time.perf_counter()
+        H1 = torch.empty(N, self.D1, dtype=torch.float32, device=dev)
+        for g in self._checked_iter(sysm, fl, rp_cpu):
+            fl.pass_a(g, H1)
+        sync()
+        t["A"], t0 = time.perf_counter() - t0, time.perf_counter()
+        G1 = torch.zeros_like(H1)
+        eat = torch.zeros(N, dtype=torch.float64, device=dev)
+        F = torch.zeros(N, 3, dtype=torch.float64, device=dev)
+        for g in self._checked_iter(sysm, fl, rp_cpu):
+            fl.pass_b(g, H1, G1, None, eat, forces=F)
+        sync()
+        t["B"], t0 = time.perf_counter() - t0, time.perf_counter()
+        for g in self._checked_iter(sysm, fl, rp_cpu):
+            fl.pass_c(g, G1, None, eat, forces=F)
+        sync()
+        t["C"] = time.perf_counter() - t0
+        eat += fl.e0[sysm.spidx.long()] + fl.shift
+        if timings is not None:
+            timings.update(t)
+        self.H1, self.G1 = H1, G1
+        return float(eat.sum()), eat, F, None
+
+    def _checked_iter(self, sysm, fl, rp_cpu):
+        for g in self._chunk_iter(sysm, fl, rp_cpu):
+            if self.check:
+                check_chunk(g, sysm.N, fl.S)
+            yield g
+
     def compute(self, sysm, graphs=None, timings=None):
-        """Returns (E float, eat fp64 [N], F fp64 [N, 3], PF fp32 [E, 3]) in the sorted index space."""
+        """Returns (E float, eat fp64 [N], F fp64 [N, 3], PF fp32 [E, 3]) in the sorted index space (PF None with
+        low_memory)."""
+        if self.low_memory:
+            if graphs is not None or getattr(sysm, "chunk_graphs", None) is not None:
+                raise ValueError("low_memory builds its chunks from a System's neighbour list")
+            return self._compute_low_memory(sysm, timings)
         fl = self._layers(sysm)
         dev, N = self.dev, sysm.N
         graphs = self._checked(graphs if graphs is not None else self.graphs(sysm), sysm, fl)

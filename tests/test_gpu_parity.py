@@ -204,6 +204,31 @@ def test_standalone_three_pass_vs_oracle(dev, model, ref_model, water_gpu, chunk
     _check(E, eat, F, _oracle_three_pass(ref_model, s, 192), s.N, rel=1e-4)
 
 
+@pytest.mark.parametrize("deterministic", [False, True])
+def test_low_memory_mode_vs_oracle_and_default(dev, model, ref_model, water_gpu, deterministic):
+    """ReceiverChunkMACE(low_memory=True): chunk topologies rebuilt per pass and each chunk's pair forces added to F
+    at once (mm_chunk_forces; the reference's _accum_forces, receiver_chunk_mace.py:272-276).  Against the oracle,
+    and against the default path: the same per-edge pair forces, summed per pass instead of once, so the forces
+    agree to fp32 rounding of PF_B + PF_C and the energies exactly (deterministic mode: bitwise)."""
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
+    s = water_gpu
+    lo = ReceiverChunkMACE(model, chunk=48, device=dev, low_memory=True, deterministic=deterministic)
+    E, eat, F, PF = lo.compute(s)
+    assert PF is None
+    _say(f"low memory (deterministic {deterministic}): E={E:.8f}")
+    _check(E, eat, F, _oracle_three_pass(ref_model, s, 192), s.N, rel=1e-4)
+    E1, eat1, F1, PF1 = ReceiverChunkMACE(model, chunk=48, device=dev, deterministic=deterministic).compute(s)
+    dF = float((F - F1).abs().max())
+    _say(f"  vs default: |dE| {abs(E - E1):.2e}, max|dF| {dF:.2e}")
+    assert dF <= 1e-6 * float(F1.abs().max())
+    if deterministic:
+        assert torch.equal(eat, eat1)
+        E2, eat2, F2, _ = lo.compute(s)
+        assert torch.equal(F2, F) and torch.equal(eat2, eat)      # bitwise repeatable
+    else:
+        assert float((eat - eat1).abs().max()) < 1e-9
+
+
 def test_fp32_vs_oracle_with_same_tables(dev, model, ref_model, water_gpu):
     """Against the fp64 oracle that uses the same 512-knot tables only fp32 rounding remains."""
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
