@@ -372,18 +372,32 @@ class ReceiverChunkMACE:
         sync()
         t["C"] = time.perf_counter() - t0
         eat = eat + fl.e0[sysm.spidx.long()] + fl.shift
-        F = pair_to_atom_forces(sysm, PF)
+        F = pair_to_atom_forces(sysm, PF, graphs)
         if timings is not None:
             timings.update(t)
         self.H1, self.G1 = H1, G1
         return float(eat.sum()), eat, F, PF[:E]
 
 
-def pair_to_atom_forces(sysm, PF):
-    """F_i = -sum_{e: recv=i} PF_e + sum_{e: send=i} PF_e (v_e = x_recv - x_send), deterministic CSR sums."""
+INT32_MAX = 2 ** 31 - 1
+
+
+def pair_to_atom_forces(sysm, PF, graphs=None):
+    """F_i = -sum_{e: recv=i} PF_e + sum_{e: send=i} PF_e (v_e = x_recv - x_send), deterministic CSR sums.  Up to
+    2^31 - 1 pairs through one sender sort of the whole list (kept on the System); beyond that, chunk by chunk
+    through each chunk's own sender CSR (mm_chunk_forces; a sort of more than 2^31 - 1 keys is not available)."""
     if getattr(sysm, "atom_forces_fn", None) is not None:     # MD pair list filtered from a skin list
         return sysm.atom_forces_fn(PF)
     dev, N = sysm.device, sysm.N
+    if sysm.send.numel() > INT32_MAX:
+        if graphs is None:
+            raise ValueError("more than 2^31 - 1 pairs: per-atom forces need the chunk topologies")
+        from .fast_layers import sender_csr
+        F = torch.zeros(N, 3, dtype=torch.float64, device=dev)
+        for g in graphs:
+            srp, sperm = sender_csr(g)
+            K.mm_chunk_forces(g.n_nodes, g.nC, g.rowptr, srp, sperm, g.nodes, PF[g.e0:g.e1], F, stream())
+        return F
     if not hasattr(sysm, "_s_perm") or sysm._s_perm_E != sysm.send.numel():
         s_perm = torch.argsort(sysm.send.long(), stable=True)
         cnt = torch.bincount(sysm.send.long(), minlength=N)

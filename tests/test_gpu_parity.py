@@ -229,6 +229,24 @@ def test_low_memory_mode_vs_oracle_and_default(dev, model, ref_model, water_gpu,
         assert float((eat - eat1).abs().max()) < 1e-9
 
 
+def test_chunked_atom_forces_beyond_int32_pairs(dev, model, water_gpu, monkeypatch):
+    """Beyond 2^31 - 1 pairs the per-atom forces are summed chunk by chunk (mm_chunk_forces over each chunk's sender
+    CSR) instead of through one sort of the whole pair list: the limit lowered to 100 pairs sends this box down
+    that path, which must give the whole-list sums to fp64 rounding (same pair forces, other summation order)."""
+    from mace_onegpu import receiver_chunk_mace as rcm
+    s = water_gpu
+    ev = rcm.ReceiverChunkMACE(model, chunk=48, device=dev, deterministic=True)
+    graphs = ev.graphs(s)
+    E, eat, F, PF = ev.compute(s, graphs=graphs)
+    monkeypatch.setattr(rcm, "INT32_MAX", 100)
+    F2 = rcm.pair_to_atom_forces(s, PF, graphs)
+    d = float((F2 - F).abs().max())
+    _say(f"  chunked force sums vs whole-list: max|dF| {d:.2e}")
+    assert d <= 1e-12 * float(F.abs().max())
+    with pytest.raises(ValueError, match="chunk topologies"):
+        rcm.pair_to_atom_forces(s, PF)
+
+
 def test_fp32_vs_oracle_with_same_tables(dev, model, ref_model, water_gpu):
     """Against the fp64 oracle that uses the same 512-knot tables only fp32 rounding remains."""
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
