@@ -65,7 +65,8 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
     harmonics are evaluated in the kernel; bwd also writes 17 floats), the 64-feature table once, B / gB
     [nC, 16, Kp] once; FLOPs = the 64 x 16 outer product (fwd) or its two transposed products (bwd) plus the
     spline evaluation.
-    tpw_*: explicit per-edge weights (FusedConvTP) -- W [E, nW, 128] and Y read once."""
+    tpw_*: explicit per-edge weights (FusedConvTP) -- W [E, nW, 128] and Y read once (backward: gW and dL/dY
+    written once)."""
     P, M = 1, 512
     if name.startswith("ace1"):
         tab_bytes = 16 * (M - 1) * 64
@@ -77,7 +78,7 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
         if name.endswith("fwd"):
             return (E * (8 + 64 + 4 * nW * C) + 4 * (nC + 1) + 4 * N * nX * C + 4 * nC * nO * C,
                     2 * E * C * nT)
-        return (E * (8 + 64 + 8 * nW * C + 8 * 16) + 4 * (nC + 1) + 8 * N * nX * C + 4 * nC * nO * C,
+        return (E * (8 + 64 + 8 * nW * C + 64) + 4 * (nC + 1) + 8 * N * nX * C + 4 * nC * nO * C,
                 2 * E * C * 3 * nT)
     gx = 1 if name == "conv2_bwd" else 0
     if name.endswith("fwd"):
@@ -690,7 +691,7 @@ def run_conv(a):
         Od = torch.empty(nN, d.nO * C, device="cuda")
         Gd = torch.randn(nN, d.nO * C, device="cuda", generator=gen2)
         gWd = torch.empty_like(Wd)
-        gYp = torch.empty(8, E, 16, device="cuda")
+        gYp = torch.empty(d.gy_parts, E, 16, device="cuda")
         gXd = torch.zeros_like(Xd)
         f = getattr(K, f"mm_{key}_fwd")
         b = getattr(K, f"mm_{key}_bwd")

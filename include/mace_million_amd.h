@@ -24,7 +24,7 @@ typedef void* mm_stream_t; /* hipStream_t */
 
 /* ---------------------------------------------------------------------------------------------- library */
 const char* mm_last_error(void);
-/* version of the argument conventions (5); a host binding must refuse a library of another version */
+/* version of the argument conventions (6); a host binding must refuse a library of another version */
 int mm_version(void);
 /* channel count (128), channel blocks (8, one per XCD) and channels per block (16) the kernels were built for */
 int mm_build_info(int* channels, int* channel_blocks, int* block_channels);
@@ -136,8 +136,9 @@ int mm_spline_coeffs_flat(const double* samples, int M, int D, double eps, doubl
  * fused_edge_conv.path_table, fused_edge_conv.py:43-68) and its autograd backward, with explicit per-edge weights
  * W [E, nW*128]: out[i] = sum over p in [rowptr[i], rowptr[i+1]) of the TP of edge e = eid[p] (eid null: e = p).
  * Tables: l1 (nX=1, nW=4, nO=16), l2 (nX=4, nW=10, nO=40), l0123 (nX=16, nW=23, nO=99); Y has 16 components.
- * Backward: gW [E, nW*128] written; gYp [8][E][16] per-channel-block partial sums of dL/dY (block stride
- * gy_cb_stride); gX [n, nX*128] accumulated with atomic adds (zero it first); a null output is skipped. */
+ * Backward: gW [E, nW*128] written; gYp [P][E][16] partial sums of dL/dY over the channel halves of a wave
+ * (P = 1 for l1, 2 for l2 and l0123; block stride gy_cb_stride; the caller sums the P rows); gX [n, nX*128]
+ * accumulated with atomic adds (zero it first); a null output is skipped. */
 int mm_tpw_l1_fwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
                   const float* W, long w_stride, const float* X, long x_stride, float* out, long out_stride,
                   mm_stream_t stream);

@@ -11,7 +11,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libmace_million_amd.so")
-ABI_VERSION = 5     # mm_version() of the library this binding's buffer layouts are written for
+ABI_VERSION = 6     # mm_version() of the library this binding's buffer layouts are written for
 
 P = ctypes.c_void_p
 I = ctypes.c_int

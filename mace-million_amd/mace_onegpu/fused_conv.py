@@ -17,11 +17,10 @@ kernels.
 """
 import torch
 
-from . import o3
+from . import codegen, o3
 from ._lib import K, stream
 
 C = 128
-N_CB = 8          # channel blocks of the kernels (one per XCD); the backward returns one dY partial per block
 
 
 class ChannelwiseTP:
@@ -39,6 +38,8 @@ class ChannelwiseTP:
         t = self.table
         self.nX, self.nW, self.nO, self.nY = t["nX"], t["nW"], t["nO"], t["nY"]
         self.weight_numel = self.nW * C
+        # the backward kernel returns dL/dY as this many partial rows per edge (one per channel half of a wave)
+        self.gy_parts = codegen.tpw_layout(t)["parts"]
 
     def require_kernel(self):
         if self.name is None:
@@ -123,7 +124,7 @@ class _FusedConvFn(torch.autograd.Function):
         n, E = X.shape[0], Y.shape[0]
         nx, ny, nw = ctx.needs_input_grad[:3]
         gX = torch.zeros_like(X) if nx else None
-        gYp = torch.empty(N_CB, E, 16, dtype=torch.float32, device=X.device) if (ny and E) else None
+        gYp = torch.empty(desc.gy_parts, E, 16, dtype=torch.float32, device=X.device) if (ny and E) else None
         gW = torch.empty_like(W) if nw else None
         if E and (nx or ny or nw):
             getattr(K, f"mm_tpw_{desc.name}_bwd")(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X,

@@ -196,6 +196,7 @@ class ReceiverChunkMACE:
         self.ace_layer1 = bool(ace_layer1)       # layer 1 in the exact density-projection form (csrc/ace.hip)
         self.dev = torch.device(device)
         self.fl = None
+        self.H1 = self.G1 = None          # H1 and G1 of the last call (kept for inspection until the next one)
         self.D1 = 4 * model.spec.C
         # keep pass A's layer-1 message and density (8 KiB per atom) so that pass C does not recompute them
         self.cache_layer1 = bool(cache_layer1) and not self.low_memory
@@ -279,6 +280,7 @@ class ReceiverChunkMACE:
         F at once (low_memory); returns (E, eat, F, None)."""
         fl = self._layers(sysm)
         dev, N = self.dev, sysm.N
+        self.H1 = self.G1 = None          # the previous call's rows go before this call allocates its own
         rp_cpu = sysm.rowptr.cpu().numpy()
         sync = torch.cuda.synchronize if timings is not None else (lambda: None)
         t, t0 = {}, time.perf_counter()
@@ -317,6 +319,7 @@ class ReceiverChunkMACE:
             if graphs is not None or getattr(sysm, "chunk_graphs", None) is not None:
                 raise ValueError("low_memory builds its chunks from a System's neighbour list")
             return self._compute_low_memory(sysm, timings)
+        self.H1 = self.G1 = None          # the previous call's rows go before this call allocates its own
         fl = self._layers(sysm)
         dev, N = self.dev, sysm.N
         graphs = self._checked(graphs if graphs is not None else self.graphs(sysm), sysm, fl)
