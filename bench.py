@@ -80,7 +80,7 @@ def conv_algorithmic(name, E, nC, N, tab, Kp=128):
                     2 * E * C * nT)
         return (E * (8 + 64 + 8 * nW * C + 64) + 4 * (nC + 1) + 8 * N * nX * C + 4 * nC * nO * C,
                 2 * E * C * 3 * nT)
-    gx = 1 if name == "conv2_bwd" else 0
+    gx = 1 if name in ("conv2_bwd", "conv0123_bwd") else 0
     if name.endswith("fwd"):
         B = 16 * E + 4 * (nC + 1) + N * (4 * nX * C + 4) + 8 * P * M * nW * C + 4 * nC * nO * C
         F = 2 * E * C * (nT + 4 * nW)
@@ -627,7 +627,7 @@ def run_ef(a):
 def run_conv(a):
     import torch
 
-    from mace_onegpu import model as mm, o3, systems
+    from mace_onegpu import codegen, model as mm, o3, systems
     from mace_onegpu._lib import K, stream
     from mace_onegpu.fused_conv import ChannelwiseTP, FusedConvTP
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
@@ -678,6 +678,33 @@ def run_conv(a):
                              fl.tables.tp1)
         calls["ace1_bwd"] = (lambda: K.mm_ace1_bwd(g.rowptr, nC, pk1, eu1, fl.tab_h, fl.S, fl.S_pad, gM1, fl.inv_h,
                                                    part, st), fl.tables.tp1)
+    # the fused spline-table convolution for the literal V3 node features 0e+1o+2e+3o (23 paths, 353 terms) on the
+    # same edge records: a 23-path table sampled from a radial network of the model's layer sizes with random
+    # weights (seed 6)
+    d3 = ChannelwiseTP([0, 1, 2, 3])
+    g6 = torch.Generator().manual_seed(6)
+    dims = [fl.spec.num_bessel] + list(fl.spec.radial_mlp) + [d3.nW * C]
+    Ws3 = [torch.randn(dims[j], dims[j + 1], generator=g6, dtype=torch.float64).cuda() for j in range(4)]
+    M = fl.M
+    r_k = torch.linspace(fl.r_lo, fl.r_hi, M, dtype=torch.float64, device="cuda")
+    eps = 1e-5 * (fl.r_hi - fl.r_lo)
+    pts = torch.cat([r_k, r_k + eps, r_k - eps]).contiguous()
+    smp = torch.empty(3 * M, d3.nW * C, dtype=torch.float64, device="cuda")
+    K.mm_radial_mlp_f64(3 * M, pts, *Ws3, fl.spec.num_bessel, dims[1], d3.nW * C, fl.spec.r_max, fl.spec.p_cutoff,
+                        mm.SILU_NORM, smp, st)
+    tab3 = torch.empty(8 * (M - 1) * d3.nW * 16 * 4, device="cuda")
+    K.mm_spline_coeffs(smp, M, d3.nW, eps, fl.h, 0, 1, tab3, st)
+    del smp
+    X3 = torch.randn(nN, d3.nX * C, device="cuda", generator=gen2)
+    gA3 = torch.randn(nC, d3.nO * C, device="cuda", generator=gen2)
+    out3 = torch.empty(nC, d3.nO * C, device="cuda")
+    n3 = codegen.tpw_layout(d3.table)["parts"]
+    part3 = torch.empty(n3 * E * 17, device="cuda")
+    gX3 = torch.zeros(nN, d3.nX * C, device="cuda")
+    calls["conv0123_fwd"] = (lambda: K.mm_conv0123_fwd(g.rowptr, nC, pk2, eu2, X3, d3.nX * C, tab3, 1, M, out3, rho,
+                                                       st), d3.table)
+    calls["conv0123_bwd"] = (lambda: K.mm_conv0123_bwd(g.rowptr, nC, pk2, eu2, X3, d3.nX * C, tab3, 1, M, fl.inv_h,
+                                                       gA3, part3, E * 17, gX3, st), d3.table)
     # explicit-weight FusedConvTP kernels (V1, V2 and the literal V3 table 0e+1o+2e+3o) on the same edges
     Y16 = torch.from_numpy(o3.spherical_harmonics(g.rij.cpu().numpy())).float().cuda()
     send = g.ls

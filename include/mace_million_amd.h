@@ -106,6 +106,15 @@ int mm_conv1_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u,
 int mm_conv2_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                  float* gX, mm_stream_t stream);
+/* The same fused convolution for the literal node features 0e+1o+2e+3o (nX=16, nW=23, nO=99, 353 terms; the
+ * reference generates ConvSpline kernels for any path table, conv_spline.py:38-181): tab with nW = 23 paths per
+ * interval row; the backward writes 6 partial rows part[h][e][17] (summed by mm_edge_grad with n_part = 6) and
+ * adds dL/dX to gX with atomic adds when gX is not null. */
+int mm_conv0123_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
+                    const float* tab, int n_tab, int M, float* out, float* rho, mm_stream_t stream);
+int mm_conv0123_bwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
+                    const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
+                    float* gX, mm_stream_t stream);
 /* Deterministic variant of mm_conv2_bwd (the reference adds dL/dX with tl.atomic_add, conv_spline.py:175-180): the
  * dL/dX of every edge goes to its own row gXe[e][0:512] instead of atomic adds into gX[send]; mm_gather_rows_csr
  * then sums the rows per sender in ascending edge order.  Same part[] output. */

@@ -51,6 +51,8 @@ SIGNATURES = {
     "mm_conv1_bwd": [P, I, P, P, P, I, P, I, I, F, P, P, L, P, P],
     "mm_conv2_bwd": [P, I, P, P, P, I, P, I, I, F, P, P, L, P, P],
     "mm_conv2_bwd_det": [P, I, P, P, P, I, P, I, I, F, P, P, L, P, P],
+    "mm_conv0123_fwd": [P, I, P, P, P, I, P, I, I, P, P, P],
+    "mm_conv0123_bwd": [P, I, P, P, P, I, P, I, I, F, P, P, L, P, P],
     "mm_gather_rows_csr": [P, P, P, L, I, P, L, I, P],
     # explicit-weight channelwise TP (generated; FusedConvTP)
     **{f"mm_tpw_{n}_fwd": [P, I, P, P, P, L, P, L, P, L, P, L, P] for n in ("l1", "l2", "l0123")},

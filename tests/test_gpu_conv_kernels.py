@@ -168,3 +168,77 @@ def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local, 
     p2 = results[0][0][:, :E * 17].view(8, E, 17).double().sum(0).cpu()
     close("dL/dY (deterministic)", p2[:, 1:], gY_r, 1e-5)
     close("inv_h dL/dt (deterministic)", p2[:, 0], inv_h * gt_r, 1e-5)
+
+
+def test_conv0123_kernels_against_oracle_tp():
+    """mm_conv0123_fwd / _bwd (literal 0e+1o+2e+3o node features: 23 paths, 353 terms, the benchmark's V3 shape)
+    against the oracle's dense channelwise TP (mace_ref.channelwise_tp over the coupling tensors, independent of
+    the generated term list) with W from the same interval coefficients in fp64, and fp64 autograd for dL/dX,
+    dL/dY and inv_h dL/dt (the latter two summed over the kernel's partial rows)."""
+    from mace_onegpu import codegen, o3
+    from mace_onegpu._lib import K, stream
+    from oracle import mace_ref
+    assert torch.cuda.is_available(), "GPU test without a GPU"
+    t3 = codegen.tpw_tables()["l0123"]
+    nX, nW, nO = t3["nX"], t3["nW"], t3["nO"]
+    parts = codegen.tpw_layout(t3)["parts"]
+    rng = np.random.default_rng(11)
+    nC, n_nodes, NR = 45, 300, 7
+    deg = rng.choice([0, 1, 2, 3, 17, 40, 65], nC)
+    send = np.concatenate([rng.choice(n_nodes, d, replace=False) for d in deg]).astype(np.int32)
+    rowptr = np.concatenate([[0], np.cumsum(deg)]).astype(np.int32)
+    E = len(send)
+    print(f"case conv0123: nC {nC} nodes {n_nodes} edges {E} parts {parts}", flush=True)
+    u = rng.normal(size=(E, 3))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    tt, row = rng.uniform(0, 1, E), rng.integers(0, NR, E)
+    dens = rng.uniform(0, 1, E)
+    X = rng.normal(size=(n_nodes, nX * C))
+    tab = rng.normal(size=(8, NR, nW, 16, 4)) * np.array([1.0, 0.5, 0.25, 0.125])
+    gA = rng.normal(size=(nC, nO * C))
+    dev = "cuda"
+    f32 = dict(dtype=torch.float32, device=dev)
+    pk = torch.empty(E, 4, **f32)
+    pk[:, 0], pk[:, 3] = torch.tensor(tt, **f32), torch.tensor(dens, **f32)
+    pk.view(torch.int32)[:, 1] = torch.tensor(row, dtype=torch.int32, device=dev)
+    pk.view(torch.int32)[:, 2] = torch.tensor(send, dtype=torch.int32, device=dev)
+    eu = torch.empty(E, 4, **f32)
+    eu[:, :3], eu[:, 3] = torch.tensor(u, **f32), 1.0
+    rp = torch.tensor(rowptr, dtype=torch.int32, device=dev)
+    Xd, tabd, gAd = torch.tensor(X, **f32), torch.tensor(tab, **f32).contiguous(), torch.tensor(gA, **f32)
+    out = torch.full((nC, nO * C), float("nan"), **f32)
+    rho = torch.full((nC,), float("nan"), **f32)
+    part = torch.full((parts, E * 17 + 3), float("nan"), **f32)
+    gX = torch.zeros(n_nodes, nX * C, **f32)
+    inv_h = 2.5
+    K.mm_conv0123_fwd(rp, nC, pk, eu, Xd, nX * C, tabd, 1, NR + 1, out, rho, stream())
+    K.mm_conv0123_bwd(rp, nC, pk, eu, Xd, nX * C, tabd, 1, NR + 1, inv_h, gAd, part, E * 17 + 3, gX, stream())
+    torch.cuda.synchronize()
+    f64 = dict(dtype=torch.float64)
+    tabc = torch.tensor(tab, **f64).float().double().permute(1, 2, 0, 3, 4).reshape(NR, nW, C, 4)
+    a = tabc[torch.from_numpy(row).long()]
+    t = torch.tensor(tt, **f64).float().double().requires_grad_()
+    tq = t[:, None, None]
+    W = a[..., 0] + tq * (a[..., 1] + tq * (a[..., 2] + tq * a[..., 3]))
+    Y = mace_ref.sh(torch.tensor(u, **f64).float().double()).detach().requires_grad_()
+    Xr = torch.tensor(X, **f64).float().double().view(n_nodes, nX, C).requires_grad_()
+    recv = torch.repeat_interleave(torch.arange(nC), torch.from_numpy(deg).long())
+    mid = mace_ref.channelwise_tp(W, Xr, Y, torch.from_numpy(send).long(), t3["paths"], t3["in_ls"], o3.coupling)
+    ref = mace_ref.scatter_sum(mid, recv, nC)
+    G = torch.tensor(gA, **f64).float().double().view(nC, nO, C)
+    (ref * G).sum().backward()
+    rho_r = torch.zeros(nC, **f64).index_add(0, recv, torch.tensor(dens, **f64).float().double())
+
+    def close(name, got, want, rel):
+        got = got.double().cpu()
+        err, scale = float((got - want).abs().max()), float(want.abs().max())
+        print(f"  {name}: max|err| {err:.3e} (max|ref| {scale:.3e})", flush=True)
+        assert torch.isfinite(got).all() and err <= rel * scale + 1e-12
+
+    close("out", out.view(nC, nO, C), ref.detach(), 1e-5)
+    close("rho", rho, rho_r, 1e-5)
+    close("gX", gX.view(n_nodes, nX, C), Xr.grad, 1e-5)
+    p = part[:, :E * 17].view(parts, E, 17).double().sum(0).cpu()
+    close("dL/dY", p[:, 1:], Y.grad, 1e-5)
+    close("inv_h dL/dt", p[:, 0], inv_h * t.grad, 1e-5)
+    assert torch.isnan(part[:, E * 17:]).all()
