@@ -117,19 +117,28 @@ def kernel_digest(kernel, read=None):
     return h.hexdigest()
 
 
+TRAFFIC_FILES = ("traffic_config5_water1M.json", "traffic_config3_water98k.json", "traffic_config4_fcc500k.json")
+
+
 def measured_traffic(kernel, workload):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes of this
-    workload (profiles/traffic_config5_water1M.json: counters scaled by a copy kernel of known size), or None
-    when no pass was recorded for this workload and the kernel's current sources."""
-    path = os.path.join(ROOT, "profiles", "traffic_config5_water1M.json")
-    if not os.path.exists(path) or kernel not in KERNEL_SOURCES:
+    workload (profiles/traffic_*.json: counters scaled by a copy kernel of known size), or None when no pass was
+    recorded for this workload and the kernel's current sources."""
+    if kernel not in KERNEL_SOURCES:
         return None
-    with open(path) as fh:
-        t = json.load(fh)
-    rec = t["kernels"].get(kernel)
-    if t["workload"] != workload or rec is None or rec.get("sources_sha256") != kernel_digest(kernel):
-        return None
-    return rec["traffic_bytes_per_launch"]
+    for name in TRAFFIC_FILES:
+        path = os.path.join(ROOT, "profiles", name)
+        if not os.path.exists(path):
+            continue
+        with open(path) as fh:
+            t = json.load(fh)
+        if t["workload"] != workload:
+            continue
+        rec = t["kernels"].get(kernel)
+        if rec is None or rec.get("sources_sha256") != kernel_digest(kernel):
+            return None
+        return rec["traffic_bytes_per_launch"]
+    return None
 
 
 def node_algorithmic(name, units, symc_flops):
@@ -584,6 +593,8 @@ def run_ef(a):
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
     value = s.N * a.steps / dt
+    if a.copy_calib_mib > 0:
+        copy_calibration(a.copy_calib_mib)
     if graphs:
         # HIP events cannot time launches inside graph replays: one eager evaluation of the same system, with every
         # launch timed, gives the per-kernel table (the same kernels the graphs replay)
@@ -614,7 +625,7 @@ def run_ef(a):
                      {"workload": workload, "atoms": s.N, "pairs": n_pairs, "chunk": chunk, "graphs": graphs,
                       "E_per_atom_eV": round(E / s.N, 8),
                       "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2)},
-                     roofline_of(kernels), kernels, cpu)
+                     roofline_of(kernels, {"config": a.config, "chunk": chunk}), kernels, cpu)
     if graphs:
         line["roofline_note"] = ("kernels timed with HIP events in one eager evaluation of the same system after the "
                                  "graph-replayed steps (events cannot time launches inside a replay)")
