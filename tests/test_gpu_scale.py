@@ -76,3 +76,26 @@ def test_config5_replica_2x2x2_reproduces_base(model, water_config5, base5):
     _say(f"  {n_pairs} pairs; |dE/N| {dE:.3e} eV, max|de_i| {de:.3e} eV, max|dF| {dF:.3e} eV/A (max|F| {Fm:.3e})")
     assert n_pairs == 8 * pairs0
     assert dE < 1e-9 and de < 1e-6 and dF < 1e-5 * Fm
+
+
+def test_config5_forces_are_the_energy_gradient(model, water_config5, base5):
+    """At production scale the forces are the derivative of the energy: for 4 atoms (O and H), central differences
+    of the total energy under displacements of +-1e-3 A along x, y and z against F.  Only the ~700 atoms within
+    2 r_max of the moved atom change their energies, and the energies are free of atomic additions (the forward
+    has none), so the difference of two 1,029,000-atom totals keeps about 1e-10 eV of noise."""
+    pos, box, Z = water_config5
+    E0, e0, F0, _ = base5
+    h = 1e-3
+    worst, Fm = 0.0, float(F0.abs().max())
+    for i in (3, 4, 514437, 1028998):
+        for d in range(3):
+            Es = []
+            for sgn in (1.0, -1.0):
+                p = pos.copy()
+                p[i, d] += sgn * h
+                Es.append(_evaluate(model, p, box, Z)[0])
+            fd = -(Es[0] - Es[1]) / (2 * h)
+            worst = max(worst, abs(fd - float(F0[i, d])))
+        _say(f"  atom {i}: F {F0[i].tolist()}")
+    _say(f"  max|F - F_fd| {worst:.3e} eV/A (max|F| {Fm:.3e})")
+    assert worst < 1e-4 * Fm
