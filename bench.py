@@ -797,7 +797,9 @@ def run_conv(a):
         oracle_check = {"receivers": nr_c, "edges": ne_c, "tolerance": 1e-4,
                         "out_max_rel": rel(out2[:nr_c].view(nr_c, 40, C), o_out),
                         "dL_dvec_max_rel": rel(PFm[:ne_c], o_gv),
-                        "dL_dX_max_rel": rel(gXm[:nn_c].view(nn_c, 4, C), o_gx)}
+                        # mm_conv2_bwd's dL/dX rows are 16-channel-block-major: gX[s][cb][k][16]
+                        "dL_dX_max_rel": rel(gXm[:nn_c].view(nn_c, 8, 4, 16).permute(0, 2, 1, 3).reshape(nn_c, 4, C),
+                                             o_gx)}
         oracle_check["pass"] = all(oracle_check[k] < 1e-4 for k in ("out_max_rel", "dL_dvec_max_rel",
                                                                       "dL_dX_max_rel"))
     line = base_line(a, "edge-conv achieved algorithmic GB/s (layer-2 forward, one 16,384-receiver chunk)", v["GBps"],

@@ -24,7 +24,7 @@ typedef void* mm_stream_t; /* hipStream_t */
 
 /* ---------------------------------------------------------------------------------------------- library */
 const char* mm_last_error(void);
-/* version of the argument conventions (6); a host binding must refuse a library of another version */
+/* version of the argument conventions (7); a host binding must refuse a library of another version */
 int mm_version(void);
 /* channel count (128), channel blocks (8, one per XCD) and channels per block (16) the kernels were built for */
 int mm_build_info(int* channels, int* channel_blocks, int* block_channels);
@@ -95,7 +95,9 @@ int mm_edge_grad(int E, const int* E_dev /* nullable */, const float* part, long
  * (spline_w.py:30-50) + FusedConvTP.forward (fused_conv.py:33-37): spline-table radial weights x channelwise TP x
  * receiver-CSR sum; and their backward (conv_spline.gen_bwd :97-181, spline_w._w_bwd :53-75): per-edge
  * dL/dr, dL/dY partials per channel block, optional dL/dX (layer 2, G1 path).  tab: interval coefficients built by
- * mm_spline_coeffs.  Layer 1: nX=1, nW=4, nO=16; layer 2: nX=4, nW=10, nO=40. */
+ * mm_spline_coeffs.  Layer 1: nX=1, nW=4, nO=16; layer 2: nX=4, nW=10, nO=40.  mm_conv2_bwd adds dL/dX with atomic
+ * adds into gX [n_nodes][512] in 16-channel-block-major rows: gX[s][cb][k][16] = dL/dX[s, k, 16 cb + j] (the
+ * channel block of one XCD contiguous per sender); mm_linear with in_cb = 4 reads that layout. */
 int mm_conv1_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                  const float* tab, int n_tab, int M, float* out, float* rho, mm_stream_t stream);
 int mm_conv2_fwd(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
@@ -116,8 +118,9 @@ int mm_conv0123_bwd(const int* rowptr, int nC, const float* e_pk, const float* e
                     const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                     float* gX, mm_stream_t stream);
 /* Deterministic variant of mm_conv2_bwd (the reference adds dL/dX with tl.atomic_add, conv_spline.py:175-180): the
- * dL/dX of every edge goes to its own row gXe[e][0:512] instead of atomic adds into gX[send]; mm_gather_rows_csr
- * then sums the rows per sender in ascending edge order.  Same part[] output. */
+ * dL/dX of every edge goes to its own row gXe[e][0:512] (16-channel-block-major, as mm_conv2_bwd's gX) instead of
+ * atomic adds into gX[send]; mm_gather_rows_csr then sums the rows per sender in ascending edge order.  Same part[]
+ * output. */
 int mm_conv2_bwd_det(const int* rowptr, int nC, const float* e_pk, const float* e_u, const float* X, int x_stride,
                      const float* tab, int n_tab, int M, float inv_h, const float* gA, float* part, long part_stride,
                      float* gXe, mm_stream_t stream);
@@ -187,12 +190,14 @@ int mm_symc2_bwd(int n, const float* x, long x_stride, const int* spec, const fl
  * planes W0 + W1 + W2 = W (fast_layers.mfma_block); products at fp32 accuracy, fp32 accumulation.  Rows: list
  * (device [n_groups][list_stride]) with list_count (device [n_groups]) selects rows per group; list_count without
  * list (n_groups 1) reads the row count from device memory, rows 0 .. list_count[0] - 1 (n_rows_max sizes the
- * launch: a captured HIP graph replays a chunk's real node count). */
+ * launch: a captured HIP graph replays a chunk's real node count).  in_cb = 0: input rows component-major (source
+ * chunk = 128 consecutive floats at in_off); in_cb = n > 0: input rows 16-channel-block-major [8][n][16] (as
+ * mm_conv2_bwd's gX), a source at in_off = 128 k being component k (k < n). */
 int mm_linear(const float* in, long in_stride, const int* in_rows, float* out, long out_stride, const int* out_rows,
               const void* W, const float* row_scale, int scale_mode, const int* list, const int* list_count,
               long list_stride, int n_groups, int w_group_stride, int n_rows_max, int accumulate, int n_comp,
               const int* comp_nsrc, const int* comp_in_off, const int* comp_w_idx, const int* comp_out_off,
-              mm_stream_t stream);
+              int in_cb, mm_stream_t stream);
 int mm_species_lists(const int* spec, int n, int S, int* lists, long stride, int* counts, mm_stream_t stream);
 /* readouts with energy accumulation and gradient: model.readouts[0] / [1] and the losses of passes B and C
  * (mliap_threepass.py:550, 578-579).  mm_readout1: eat[i] += scale h1[i, 0:128] . w0 and, when gh is not null,

@@ -27,7 +27,8 @@ extern "C" const char* mm_last_error(void) { return g_last_error.c_str(); }
 // planes.  3: mm_ace1_fwd / mm_ace1_bwd take the edge vectors (unit vector, r) instead of stored harmonics.
 // 4: the edge-geometry and edge-gradient entry points take a device edge count.  5: mm_ace1_bwd reads gB in its
 // MFMA operand order.  6: the mm_tpw_*_bwd kernels write one dL/dY partial per channel half (1 or 2), not 8.
-extern "C" int mm_version(void) { return 6; }
+// 7: mm_conv2_bwd / mm_conv2_bwd_det write dL/dX in 16-channel-block-major rows; mm_linear takes in_cb.
+extern "C" int mm_version(void) { return 7; }
 
 // Channel count and channel-block geometry the generated kernels were built for.
 extern "C" int mm_build_info(int* channels, int* channel_blocks, int* block_channels) {

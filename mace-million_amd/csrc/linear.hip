@@ -62,6 +62,8 @@ struct MMLinArgs {
   long list_stride;
   int n_rows;             // without list
   int w_group_stride;     // weight block offset of group g (species)
+  int in_cb;              // 0: input rows component-major; n > 0: 16-channel-block-major rows [8][n][16], a
+                          // source chunk at in_off = 128 k being component k of every block
   int accumulate;
   int n_comp;
   MMLinComp comp[MM_LIN_MAX_COMP];
@@ -85,15 +87,21 @@ __device__ __forceinline__ void mm_lin_rows(const MMLinArgs& args, const int* li
 // bytes of a row.  (In the MFMA operand layout the 16 lanes of a row group would read 16 different rows, which the
 // texture path serves one lane per clock.)  mm_lin_stage_a passes step t through the wave's LDS rows into the
 // operand layout.
+// With channel-block-major input rows (in_cb = n components per block), chunk float q = 32 t + 4 (L & 7) of
+// component k lies at (q >> 4) 16 n + 16 k + (q & 15): every lane's 4 floats stay contiguous.
 __device__ __forceinline__ void mm_lin_load_a(const MMLinArgs& args, const MMLinRows& rw, int in_off, int lane,
                                               floatx4 (&a)[8]) {
   const long r0 = __shfl(rw.in_row, lane >> 3), r1 = __shfl(rw.in_row, 8 + (lane >> 3));
-  const float* __restrict__ p0 = args.in + r0 * args.in_stride + in_off + 4 * (lane & 7);
-  const float* __restrict__ p1 = args.in + r1 * args.in_stride + in_off + 4 * (lane & 7);
+  const int qb = 4 * (lane & 7);
+  const int n = args.in_cb;
+  const int base = n ? (qb >> 4) * 16 * n + 16 * (in_off >> 7) + (qb & 15) : in_off + qb;
+  const int tstep = n ? 32 * n : 32;
+  const float* __restrict__ p0 = args.in + r0 * args.in_stride + base;
+  const float* __restrict__ p1 = args.in + r1 * args.in_stride + base;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    a[2 * t] = *(const floatx4*)(p0 + 32 * t);
-    a[2 * t + 1] = *(const floatx4*)(p1 + 32 * t);
+    a[2 * t] = *(const floatx4*)(p0 + tstep * t);
+    a[2 * t + 1] = *(const floatx4*)(p1 + tstep * t);
   }
 }
 
@@ -221,7 +229,7 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
                          const int* out_rows, const void* W, const float* row_scale, int scale_mode,
                          const int* list, const int* list_count, long list_stride, int n_groups, int w_group_stride,
                          int n_rows_max, int accumulate, int n_comp, const int* comp_nsrc, const int* comp_in_off,
-                         const int* comp_w_idx, const int* comp_out_off, hipStream_t stream) {
+                         const int* comp_w_idx, const int* comp_out_off, int in_cb, hipStream_t stream) {
   MM_CHECK_ARG(n_comp >= 1 && n_comp <= MM_LIN_MAX_COMP, "n_comp out of range");
   MM_CHECK_ARG(n_groups >= 1 && n_rows_max >= 0, "bad sizes");
   MM_CHECK_ARG(list == nullptr || list_count != nullptr, "a row list needs its counts");
@@ -229,6 +237,8 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
                "one group");
   MM_CHECK_ARG(list != nullptr || n_groups == 1, "groups need row lists");
   MM_CHECK_ARG(in_stride % 4 == 0, "input row stride must be a multiple of 4 floats");
+  MM_CHECK_ARG(in_cb >= 0 && (in_cb == 0 || in_stride >= 128L * in_cb), "channel-block-major rows: in_cb >= 0 "
+               "components per block, rows of at least 128 in_cb floats");
   MMLinArgs a;
   a.in = in;
   a.in_stride = in_stride;
@@ -244,6 +254,7 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
   a.list_stride = list_stride;
   a.n_rows = n_rows_max;
   a.w_group_stride = w_group_stride;
+  a.in_cb = in_cb;
   a.accumulate = accumulate;
   a.n_comp = n_comp;
   for (int j = 0; j < n_comp; ++j) {
@@ -253,6 +264,8 @@ extern "C" int mm_linear(const float* in, long in_stride, const int* in_rows, fl
       a.comp[j].in_off[q] = comp_in_off[j * MM_LIN_MAX_SRC + q];
       a.comp[j].w_idx[q] = comp_w_idx[j * MM_LIN_MAX_SRC + q];
       MM_CHECK_ARG(q >= comp_nsrc[j] || a.comp[j].in_off[q] % 4 == 0, "source offsets must be multiples of 4");
+      MM_CHECK_ARG(q >= comp_nsrc[j] || in_cb == 0 || (a.comp[j].in_off[q] % 128 == 0 &&
+                   a.comp[j].in_off[q] / 128 < in_cb), "channel-block-major sources are whole components < in_cb");
     }
     a.comp[j].out_off = comp_out_off[j];
   }

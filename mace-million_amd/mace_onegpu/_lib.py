@@ -11,7 +11,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(HERE), "lib", "libmace_million_amd.so")
-ABI_VERSION = 6     # mm_version() of the library this binding's buffer layouts are written for
+ABI_VERSION = 7     # mm_version() of the library this binding's buffer layouts are written for
 
 P = ctypes.c_void_p
 I = ctypes.c_int
@@ -63,7 +63,7 @@ SIGNATURES = {
     "mm_symc1_bwd": [I, P, L, P, P, P, L, P, L, P, P, P],
     "mm_symc2_bwd": [I, P, L, P, P, P, L, P, L, P, P, P],
     # node level
-    "mm_linear": [P, L, P, P, L, P, P, P, I, P, P, L, I, I, I, I, I, P, P, P, P, P],
+    "mm_linear": [P, L, P, P, L, P, P, P, I, P, P, L, I, I, I, I, I, P, P, P, P, I, P],
     "mm_fill_f32": [P, L, F, P],
     "mm_fill_f64": [P, L, D, P],
     "mm_fill_i32": [P, L, I, P],

@@ -366,18 +366,19 @@ class FastLayers:
 
     # ------------------------------------------------------------------ helpers
     def _lin(self, plan, inp, in_stride, out, out_stride, W, rows, in_rows=None, out_rows=None, scale=None,
-             scale_mode=0, species=False, accumulate=0, w_group_stride=0, count_dev=None):
-        """count_dev (optional device int32 [1]): the row count read by the kernel, rows only sizing the launch."""
+             scale_mode=0, species=False, accumulate=0, w_group_stride=0, count_dev=None, in_cb=0):
+        """count_dev (optional device int32 [1]): the row count read by the kernel, rows only sizing the launch.
+        in_cb: input rows in 16-channel-block-major order with in_cb components (mm_conv2_bwd's dL/dX)."""
         ws = self.ws
         units = (rows, plan.k_sum, plan.n_in, plan.n, accumulate, plan.n_w * (self.S if species else 1))
         if species:
             self._timed("linear", units, K.mm_linear, inp, in_stride, in_rows, out, out_stride, out_rows, W, scale,
                         scale_mode, ws["lists"], ws["counts"], ws["lists_stride"], self.S, w_group_stride, rows,
-                        accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, stream())
+                        accumulate, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, in_cb, stream())
         else:
             self._timed("linear", units, K.mm_linear, inp, in_stride, in_rows, out, out_stride, out_rows, W, scale,
                         scale_mode, None, count_dev, 0, 1, 0, rows, accumulate, plan.n, plan.nsrc, plan.inoff,
-                        plan.widx, plan.outoff, stream())
+                        plan.widx, plan.outoff, in_cb, stream())
 
     def _geometry(self, k, g):
         """Edge geometry of chunk g for interaction block k (LAMMPS pair vectors or positions)."""
@@ -533,7 +534,8 @@ class FastLayers:
                        pf, 0, stream())
         if forces is not None:
             self._add_chunk_forces(g, pf, forces)
+        # gXh holds dL/dX in 16-channel-block-major rows (as mm_conv2_bwd / mm_conv2_bwd_det write it)
         self._lin(self.plan_p1, ws["gXh"], D1, G1, D1, self.W_up2T, g.n_nodes, out_rows=g.nodes, accumulate=1,
-                  count_dev=g.N_dev)
+                  count_dev=g.N_dev, in_cb=4)
         self._lin(self.plan_sk1, gh2, C, G1, D1, self.W_sk1T, g.nC, out_rows=g.nodes, species=True, w_group_stride=1,
                   accumulate=1)

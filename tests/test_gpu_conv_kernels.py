@@ -141,7 +141,11 @@ def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local, 
     # race error is of the order of the values themselves)
     close("out", out.view(nC, 40, C), out_r, 1e-5)
     close("rho", rho, rho_r, 1e-5)
-    close("gX", gX, gX_r, 1e-5)
+    # dL/dX comes in 16-channel-block-major rows, gX[s][cb][k][16] = dL/dX[s, k, 16 cb + j]
+    def comp_major(g):
+        return g.view(-1, 8, 4, 16).permute(0, 2, 1, 3).reshape(-1, 4 * C)
+
+    close("gX", comp_major(gX), gX_r, 1e-5)
     p = part[:, :E * 17].view(8, E, 17).double().sum(0).cpu()
     close("dL/dY", p[:, 1:], gY_r, 1e-5)
     close("inv_h dL/dt", p[:, 0], inv_h * gt_r, 1e-5)
@@ -162,7 +166,7 @@ def test_conv2_kernels_against_fp64_autograd(name, nC, n_nodes, deg_max, local, 
         K.mm_gather_rows_csr(srp, sperm, gXe, 4 * C, 4 * C, gX2, 4 * C, n_nodes, stream())
         torch.cuda.synchronize()
         results.append((part2.clone(), gX2.clone()))
-    close("gX (deterministic)", gX2, gX_r, 1e-5)
+    close("gX (deterministic)", comp_major(gX2), gX_r, 1e-5)
     assert torch.equal(results[0][1], results[1][1])                # bitwise repeatable
     assert torch.equal(results[0][0][:, :E * 17], results[1][0][:, :E * 17])
     p2 = results[0][0][:, :E * 17].view(8, E, 17).double().sum(0).cpu()

@@ -118,7 +118,7 @@ def test_mfma_linear_against_torch(dev):
     counts = torch.zeros(S, dtype=torch.int32, device=dev)
     _lib.K.mm_species_lists(spec.int().to(dev), n, S, lists, n, counts, _lib.stream())
     _lib.K.mm_linear(x.float().to(dev), 768, None, out, 384, None, W, rho.float().to(dev), 1, lists, counts, n, S, 2, n,
-                     1, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, _lib.stream())
+                     1, plan.n, plan.nsrc, plan.inoff, plan.widx, plan.outoff, 0, _lib.stream())
     ref = out0.clone()
     inv = 1.0 / (rho + 1)
     for i in range(n):
@@ -153,13 +153,33 @@ def test_mfma_linear_against_torch(dev):
     a = torch.full((n, 128), float("nan"), device=dev)
     b = torch.full((n, 128), float("nan"), device=dev)
     _lib.K.mm_linear(xs, 128, None, a, 128, None, W, None, 0, None, None, 0, 1, 0, n_dev, 0, p1.n, p1.nsrc,
-                     p1.inoff, p1.widx, p1.outoff, _lib.stream())
+                     p1.inoff, p1.widx, p1.outoff, 0, _lib.stream())
     _lib.K.mm_linear(xs, 128, None, b, 128, None, W, None, 0, None,
                      torch.tensor([n_dev], dtype=torch.int32, device=dev), 0, 1, 0, n, 0, p1.n, p1.nsrc, p1.inoff,
-                     p1.widx, p1.outoff, _lib.stream())
+                     p1.widx, p1.outoff, 0, _lib.stream())
     torch.cuda.synchronize()
     assert torch.equal(a[:n_dev], b[:n_dev]) and bool(torch.isfinite(b[:n_dev]).all())
     assert bool(b[n_dev:].isnan().all())
+    # 16-channel-block-major input rows (in_cb, the layout of mm_conv2_bwd's dL/dX): the same sums, bit for bit, as
+    # the component-major rows they permute; row gathers and 4 components of which 3 share a weight block
+    x4 = x[:, :512].float().to(dev).contiguous()                               # [n, 4 components x 128]
+    x4cb = x4.view(n, 4, 8, 16).permute(0, 2, 1, 3).contiguous().view(n, 512)  # [n, 8 blocks x 4 x 16]
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(3))[:200].int().to(dev)
+    p4 = LinPlan([(0, [(0, 0)]), (128, [(128, 1)]), (256, [(256, 1)]), (384, [(384, 1)])])
+    c0 = torch.empty(200, 512, device=dev)
+    c1 = torch.empty(200, 512, device=dev)
+    _lib.K.mm_linear(x4, 512, rows, c0, 512, None, W, None, 0, None, None, 0, 1, 0, 200, 0, p4.n, p4.nsrc,
+                     p4.inoff, p4.widx, p4.outoff, 0, _lib.stream())
+    _lib.K.mm_linear(x4cb, 512, rows, c1, 512, None, W, None, 0, None, None, 0, 1, 0, 200, 0, p4.n, p4.nsrc,
+                     p4.inoff, p4.widx, p4.outoff, 4, _lib.stream())
+    torch.cuda.synchronize()
+    assert torch.equal(c0, c1)
+    ref4 = torch.cat([x[rows.long().cpu(), 0:128] @ Ws[0]] + [x[rows.long().cpu(), 128 * k:128 * k + 128] @ Ws[1]
+                                                              for k in (1, 2, 3)], dim=1)
+    assert float((c1.double().cpu() - ref4).abs().max() / ref4.abs().max()) < 2e-6
+    with pytest.raises(RuntimeError, match="channel-block-major"):
+        _lib.K.mm_linear(x4cb, 512, None, c1, 512, None, W, None, 0, None, None, 0, 1, 0, 200, 0, p4.n, p4.nsrc,
+                         p4.inoff, p4.widx, p4.outoff, 3, _lib.stream())
 
 
 def test_spline_tables_against_oracle_hermite(dev, model, ref_model):
