@@ -127,8 +127,9 @@ __device__ __forceinline__ void mm_split3_bf16(const floatx8& x, bf16x8& x0, bf1
   x2 = __builtin_convertvector(r2, bf16x8);
 }
 
-// A workgroup handles n_blk consecutive row blocks of one output component; with a single source the weight block
-// is staged in LDS once for all of them.
+// A workgroup handles n_blk consecutive row blocks of one output component.  A weight block is staged in LDS only
+// when it is not the one already there: once for all row blocks with a single source, n_src - 1 times per row block
+// after the first with several (their order alternates between row blocks).
 __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs args, int n_blk) {
   __shared__ uint4 Wl[3 * 2048];
   __shared__ float As_all[MM_LIN_NW * 16 * MM_LIN_AS];   // per wave: 16 rows of one K-step
@@ -142,7 +143,7 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
   float* __restrict__ as = As_all + wave * 16 * MM_LIN_AS;
   const int n_src = cp.n_src;
-  const bool restage = n_src > 1;
+  int staged = -1;   // weight block held in LDS (wave-uniform)
   MMLinRows rw;
   mm_lin_rows(args, list, nrows, blk0 * MM_LIN_BLOCK_ROWS, wave, i, rw);
   for (int blk = blk0; blk < blk1; ++blk) {
@@ -150,14 +151,20 @@ __global__ void __launch_bounds__(64 * MM_LIN_NW) mm_linear_kernel(MMLinArgs arg
     floatx4 acc[8];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int q = 0; q < n_src; ++q) {
+    // odd row blocks take the sources in reverse order, so that the block in LDS at the end of one row block is
+    // the first one the next needs (n_src - 1 stagings per row block instead of n_src; the order depends only on
+    // the row block, so every launch partition sums a row in the same order)
+    for (int qq = 0; qq < n_src; ++qq) {
+      const int q = (blk & 1) ? n_src - 1 - qq : qq;
       floatx4 a[8];
       mm_lin_load_a(args, rw, cp.in_off[q], lane, a);
-      if (restage || blk == blk0) {
-        const uint4* __restrict__ Wg = args.W + (size_t)(cp.w_idx[q] + grp * args.w_group_stride) * 6144;
+      const int widx = cp.w_idx[q] + grp * args.w_group_stride;
+      if (widx != staged) {
+        const uint4* __restrict__ Wg = args.W + (size_t)widx * 6144;
         __syncthreads();
         for (int j = threadIdx.x; j < 6144; j += 64 * MM_LIN_NW) Wl[j] = Wg[j];
         __syncthreads();
+        staged = widx;
       }
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
