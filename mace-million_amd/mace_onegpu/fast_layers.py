@@ -18,7 +18,6 @@ linear and skip_tp of layer 1 are both linear per (l, species) and act back to b
 import ctypes
 import math
 
-import numpy as np
 import torch
 
 from . import codegen, model as mm

@@ -12,11 +12,9 @@ update_pair_forces_gpu(PF).  This class builds the same object without LAMMPS:
   * update_pair_forces_gpu keeps PF and assembles per-atom forces the way LAMMPS does
     (f_i -= PF, f_j += PF, then ghost forces summed onto owners).
 """
-import numpy as np
 import torch
 
 from ._lib import K, stream
-from .receiver_chunk_mace import System
 
 
 class PeriodicMLIAPData:

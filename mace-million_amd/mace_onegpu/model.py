@@ -26,7 +26,6 @@ radial-MLP output and the density (mace's ``cutoff is not None`` branch, fast_la
 constant by quadrature.
 Features are stored "ir_mul" (component-major, channel-minor), as in the reference (make_threepass_model.py:42).
 """
-import math
 
 import torch
 

@@ -3,7 +3,6 @@ the HIP kernels against the fp64 CPU oracle (oracle.mace_ref.channelwise_tp + sc
 
 Tolerance (fp32 kernels vs fp64 oracle, sums of <= 353 terms over <= 40 edges): max|d| <= 2e-5 * max|ref|.
 """
-import numpy as np
 import pytest
 import torch
 
