@@ -9,6 +9,8 @@ ReceiverChunkMACE at the production chunk of 131,072 receivers (about 11.8 M edg
   per-atom energy and force of its base image.  The two evaluations run the same fp32 arithmetic in different
   orders (other Morton orders, chunk boundaries and atomic-add orders), so they agree to fp32 rounding.
 * Forces against 4-point central differences of the 1,029,000-atom total energy, for 4 atoms.
+* The same box as two chunks of 514,500 receivers, whose buffers exceed 2^31 - 1 elements, against the production
+  chunk.
 """
 import numpy as np
 import pytest
@@ -23,12 +25,12 @@ def _say(*a):
     print(*a, flush=True)
 
 
-def _evaluate(model, pos, box, Z):
+def _evaluate(model, pos, box, Z, chunk=CHUNK):
     """(E, per-atom energies, forces) in the input atom order, on the host."""
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
     s = System(pos, box, Z - 1, 6.0, "cuda")
     s.build_neighbors()
-    ev = ReceiverChunkMACE(model, chunk=CHUNK, device="cuda")
+    ev = ReceiverChunkMACE(model, chunk=chunk, device="cuda")
     E, eat, F, PF = ev.compute(s)
     perm = s.perm.long()
     eo, Fo = torch.empty_like(eat), torch.empty_like(F)
@@ -77,6 +79,27 @@ def test_config5_replica_2x2x2_reproduces_base(model, water_config5, base5):
     _say(f"  {n_pairs} pairs; |dE/N| {dE:.3e} eV, max|de_i| {de:.3e} eV, max|dF| {dF:.3e} eV/A (max|F| {Fm:.3e})")
     assert n_pairs == 8 * pairs0
     assert dE < 1e-9 and de < 1e-6 and dF < 1e-5 * Fm
+
+
+def test_config5_two_chunks_beyond_32_bit_buffers(model, water_config5, base5):
+    """The same box as two chunks of 514,500 receivers (about 46 M edges each).  A chunk's layer-2 message and
+    cotangent buffers then hold 514,500 x 5,120 = 2.6e9 floats and its backward partial rows 8 x 46 M x 17 = 6.3e9,
+    beyond 2^31 - 1 elements, so the kernels' index arithmetic past 32 bits is exercised.  Against the production
+    chunk: the per-atom energies to fp32 rounding (the linears sum a row's sources in an order that depends on the
+    row's block within the chunk) and the forces to fp32 rounding (the sender-feature gradient's float atomics are
+    summed in another order)."""
+    pos, box, Z = water_config5
+    E0, e0, F0, pairs0 = base5
+    big = (len(pos) + 1) // 2
+    _say(f"case config5 two chunks of {big}")
+    E, eat, F, n_pairs = _evaluate(model, pos, box, Z, chunk=big)
+    assert big * 5120 > 2 ** 31 and 8 * 17 * (n_pairs // 2) > 2 ** 31
+    de = float((eat - e0).abs().max())
+    dF = float((F - F0).abs().max())
+    Fm = float(F0.abs().max())
+    _say(f"  |dE| {abs(E - E0):.3e} eV, max|de_i| {de:.3e} eV, max|dF| {dF:.3e} eV/A (max|F| {Fm:.3e})")
+    assert n_pairs == pairs0
+    assert abs(E - E0) < 1e-6 and de < 1e-6 and dF < 1e-5 * Fm
 
 
 def test_config5_forces_are_the_energy_gradient(model, water_config5, base5):
