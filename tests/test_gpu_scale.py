@@ -11,6 +11,8 @@ ReceiverChunkMACE at the production chunk of 131,072 receivers (about 11.8 M edg
 * Forces against 4-point central differences of the 1,029,000-atom total energy, for 4 atoms.
 * The same box as two chunks of 514,500 receivers, whose buffers exceed 2^31 - 1 elements, against the production
   chunk.
+* Configuration 4 (500,000-atom FCC, four species) at full size: per-atom energies against the oracle and a
+  finite-difference force.
 """
 import numpy as np
 import pytest
@@ -127,3 +129,35 @@ def test_config5_forces_are_the_energy_gradient(model, water_config5, base5):
         _say(f"  atom {i}: F {F0[i].tolist()}  F_fd {fd}")
     _say(f"  max|F - F_fd| {worst:.3e} eV/A (max|F| {Fm:.3e})")
     assert worst < 5e-5
+
+
+def test_config4_per_atom_energies_and_forces_at_full_size(model, ref_model):
+    """Configuration 4 at full size: the 500,000-atom FCC Fe/Ni/Cr/Co box (four species: the species-block skip,
+    the per-species symmetric contractions and the four-species ACE layer 1) at chunk 131072.  Per-atom energies of
+    16 atoms, 4 of each species, against the fp64 oracle on each atom's own 2 r_max neighbourhood (bar 1e-5 eV),
+    and the force of one Cr atom against the 4-point central difference of the total energy (h = 1e-2 A; bar
+    5e-5 eV/A, as for configuration 5)."""
+    from mace_onegpu import systems
+    from oracle import mace_ref
+    pos, box, Z = systems.fcc_alloy(n_cells=50)
+    _say(f"case config4 FCC: {len(pos)} atoms")
+    E0, e0, F0, n_pairs = _evaluate(model, pos, box, Z)
+    rng = np.random.default_rng(12)
+    idx = [int(rng.choice(np.nonzero(Z == z)[0])) for z in (26, 28, 24, 27) for _ in range(4)]
+    worst = 0.0
+    for i in idx:
+        worst = max(worst, abs(float(e0[i]) - mace_ref.atom_energy_local(ref_model, pos, box, Z - 1, i)))
+    _say(f"  {n_pairs} pairs; 16 atoms: max|e_gpu - e_oracle| {worst:.3e} eV")
+    assert worst < 1e-5
+    i, h = idx[8], 1e-2
+    fd = []
+    for d in range(3):
+        E = {}
+        for k in (1, -1, 2, -2):
+            p = pos.copy()
+            p[i, d] += k * h
+            E[k] = _evaluate(model, p, box, Z)[0]
+        fd.append(-(8 * (E[1] - E[-1]) - (E[2] - E[-2])) / (12 * h))
+    err = float(np.abs(np.array(fd) - F0[i].numpy()).max())
+    _say(f"  atom {i} (Z {Z[i]}): F {F0[i].tolist()}  F_fd {fd}; max|F - F_fd| {err:.3e} eV/A")
+    assert err < 5e-5
