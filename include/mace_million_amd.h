@@ -148,9 +148,12 @@ int mm_spline_coeffs_flat(const double* samples, int M, int D, double eps, doubl
  * fused_edge_conv.path_table, fused_edge_conv.py:43-68) and its autograd backward, with explicit per-edge weights
  * W [E, nW*128]: out[i] = sum over p in [rowptr[i], rowptr[i+1]) of the TP of edge e = eid[p] (eid null: e = p).
  * Tables: l1 (nX=1, nW=4, nO=16), l2 (nX=4, nW=10, nO=40), l0123 (nX=16, nW=23, nO=99); Y has 16 components.
- * Backward: gW [E, nW*128] written; gYp [P][E][16] partial sums of dL/dY over the channel halves of a wave
- * (P = 1 for l1, 2 for l2 and l0123; block stride gy_cb_stride; the caller sums the P rows); gX [n, nX*128]
- * accumulated with atomic adds (zero it first); a null output is skipped. */
+ * Backward: gW [E, nW*128] written; gYp [P][E][16] partial sums of dL/dY, one row per channel half and path group
+ * of the kernel (P = 1 for l1, 2 for l2, 6 for l0123; block stride gy_cb_stride; the caller sums the P rows); gX
+ * [n, nX*128] accumulated with atomic adds (zero it first); a null output is skipped.
+ * Other tables (harmonics up to l = 3): the same two entry points, named mm_tpw_j<hash>_fwd / _bwd, are exported
+ * by lib/jit/tpw_j<hash>.so, which mace_onegpu.tp_jit generates and compiles for the table on first use (P from
+ * codegen.tpw_layout(table)["parts"]). */
 int mm_tpw_l1_fwd(const int* rowptr, int nR, const int* eid, const int* send, const float* Y, long y_stride,
                   const float* W, long w_stride, const float* X, long x_stride, float* out, long out_stride,
                   mm_stream_t stream);

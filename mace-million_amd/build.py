@@ -2,9 +2,10 @@
 
     python mace-million_amd/build.py            (also called by __graft_entry__.build())
 
-Output: mace-million_amd/lib/libmace_million_amd.so (git-ignored; it travels with the tree to the GPU box), and
+Output: mace-million_amd/lib/libmace_million_amd.so (git-ignored; it travels with the tree to the GPU box),
 lib/kernel_ops.json: the fp32 operations per thread that the straight-line generated symmetric-contraction kernels
-execute, counted from their gfx950 assembly (bench.py reports their FLOP rates from it).
+execute, counted from their gfx950 assembly (bench.py reports their FLOP rates from it), and lib/jit/: the
+channelwise TP kernels of the path tables in o3.PREBUILT_JIT_TP_TABLES (mace_onegpu/tp_jit.py).
 Every HIP source is compiled with -Xclang -target-feature -Xclang -packed-fp32-ops (no packed-FP32 instructions)
 and -munsafe-fp-atomics (hardware float atomics instead of compare-and-swap loops).
 """
@@ -88,12 +89,19 @@ def build(jobs=None, verbose=True):
     os.makedirs(LIB_DIR, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(8, os.cpu_count() or 4)
+    sys.path.insert(0, HERE)
+    from mace_onegpu import o3, tp_jit
+
     with ThreadPoolExecutor(jobs) as ex:
         counts = [ex.submit(_count_ops, n) for n in COUNTED]
+        # the kernels of the tables that FusedConvTP builds on first use, made ahead for the listed tables
+        jit = [ex.submit(tp_jit.build, o3.tp_table(list(a), b, c), True) for a, b, c in o3.PREBUILT_JIT_TP_TABLES]
         objs = list(ex.map(_compile, srcs))
         ops = {}
         for c in counts:
             ops.update(c.result())
+        for j in jit:
+            j.result()
     import json
     with open(OPS_JSON, "w") as fh:
         json.dump(ops, fh, indent=1)

@@ -3,6 +3,7 @@
 Module map (mirrors the reference package mace_onegpu, same module paths for the drop-in API):
   mliap_threepass   ThreePassMLIAP: LAMMPS ML-IAP unified plugin, compute_forces(data)
   fused_conv        FusedConvTP: channelwise TP + receiver scatter as an nn.Module
+  tp_jit            kernels of path tables without a compiled kernel, built on first use
   receiver_chunk_mace  System (GPU cell-list neighbours), ReceiverChunkMACE (standalone three-pass)
   chunk_graphs      ChunkGraphExec: HIP-graph capture and replay of the passes of full receiver chunks
   md                MDRunner: velocity-Verlet MD with a skin neighbour list (the standalone MD-loop shape)

@@ -85,8 +85,11 @@ _lib = None
 
 
 class _Fn:
-    def __init__(self, name, fn):
-        self.name, self.fn = name, fn
+    """A C-ABI entry point: device tensors passed as pointers, a nonzero status raised with the message of the
+    library's mm_last_error() (err; the main library's by default)."""
+
+    def __init__(self, name, fn, err=None):
+        self.name, self.fn, self.err = name, fn, err
 
     def __call__(self, *args):
         conv = []
@@ -103,7 +106,7 @@ class _Fn:
                 conv.append(a)
         rc = self.fn(*conv)
         if rc != 0:
-            raise RuntimeError(f"{self.name} failed ({rc}): {last_error()}")
+            raise RuntimeError(f"{self.name} failed ({rc}): {(self.err or last_error)()}")
         return rc
 
 

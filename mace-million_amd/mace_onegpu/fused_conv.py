@@ -11,7 +11,8 @@ The reference hands the three inputs to a cuEquivariance SegmentedPolynomial bui
 cue.descriptors.channelwise_tensor_product(...).flatten_coefficient_modes().squeeze_modes()
 (fused_edge_conv.py:43-68); here the descriptor is ChannelwiseTP (the same term list, from
 mace_onegpu.o3.tp_table) and the arithmetic runs in the generated kernels mm_tpw_<table>_{fwd,bwd}
-(receiver-CSR over a stable receiver order, so edges may arrive in any order).  Backward (autograd) gives
+(receiver-CSR over a stable receiver order, so edges may arrive in any order; tables without a kernel in the
+library get theirs built on first use, tp_jit).  Backward (autograd) gives
 d node_feats (atomic adds on senders), d edge_attrs and d tp_weights.  fp32 only, as the reference's fused
 kernels.
 """
@@ -25,8 +26,9 @@ C = 128
 
 class ChannelwiseTP:
     """Channelwise TP descriptor: node-feature irreps in_ls (C channels each) x spherical harmonics 0..sh_lmax ->
-    mid irreps (l3 in target_ls), e3nn/MACE path order (o3.tp_paths).  Only tables with a compiled kernel
-    (o3.COMPILED_TP_TABLES) can be evaluated."""
+    mid irreps (l3 in target_ls), e3nn/MACE path order (o3.tp_paths).  The tables of o3.COMPILED_TP_TABLES run
+    the library's kernels; any other table with harmonics up to l = 3 runs kernels generated and built for it on
+    first use (tp_jit)."""
 
     def __init__(self, in_ls, sh_lmax=3, target_ls=(0, 1, 2, 3)):
         self.in_ls, self.sh_lmax, self.target_ls = tuple(in_ls), int(sh_lmax), tuple(target_ls)
@@ -41,19 +43,21 @@ class ChannelwiseTP:
         # the backward kernel returns dL/dY as this many partial rows per edge (one per channel half of a wave)
         self.gy_parts = codegen.tpw_layout(t)["parts"]
 
-    def require_kernel(self):
-        if self.name is None:
-            raise NotImplementedError(
-                f"no compiled kernel for the channelwise TP {self.in_ls} x Y(l<={self.sh_lmax}) -> {self.target_ls}; "
-                f"compiled tables: {sorted(o3.COMPILED_TP_TABLES)} (add the table to o3.COMPILED_TP_TABLES and "
-                f"rebuild the library)")
+    def kernels(self):
+        """(forward, backward) entry points of this table (arguments of mm_tpw_l1_fwd / _bwd): the library's for a
+        compiled table, else those built for the table (tp_jit; the first use builds them)."""
         if self.nY != 16:
-            raise NotImplementedError("the compiled kernels read 16 spherical-harmonic components (l <= 3)")
-        return self.name
+            raise NotImplementedError("the kernels read 16 spherical-harmonic components (l <= 3), "
+                                      f"not {self.nY} (sh_lmax = {self.sh_lmax})")
+        if self.name is not None:
+            return getattr(K, f"mm_tpw_{self.name}_fwd"), getattr(K, f"mm_tpw_{self.name}_bwd")
+        from . import tp_jit
+        return tp_jit.kernels(self.table)
 
     def __repr__(self):
+        kern = self.name if self.name is not None else "built on first use"
         return (f"ChannelwiseTP(in_ls={self.in_ls}, sh_lmax={self.sh_lmax}, target_ls={self.target_ls}; nX={self.nX}, "
-                f"nW={self.nW}, nO={self.nO}, terms={len(self.table['terms'])}, kernel={self.name})")
+                f"nW={self.nW}, nO={self.nO}, terms={len(self.table['terms'])}, kernel={kern})")
 
 
 def receiver_csr(edge_index, n_nodes, n_send_rows):
@@ -97,7 +101,7 @@ def _check(t, name, cols):
 class _FusedConvFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, X, Y, W, edge_index, desc):
-        name = desc.require_kernel()
+        fwd, bwd = desc.kernels()
         X = _check(X, "node_feats", desc.nX * C)
         Y = _check(Y, "edge_attrs", desc.nY)
         W = _check(W, "tp_weights", desc.nW * C)
@@ -107,11 +111,10 @@ class _FusedConvFn(torch.autograd.Function):
         n = X.shape[0]
         rowptr, eid, send = receiver_csr(edge_index, n, n)
         out = torch.empty(n, desc.nO * C, dtype=torch.float32, device=X.device)
-        getattr(K, f"mm_tpw_{name}_fwd")(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X, X.stride(0), out,
-                                         out.stride(0), stream())
+        fwd(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X, X.stride(0), out, out.stride(0), stream())
         ctx.save_for_backward(X, Y, W, rowptr, send, eid if eid is not None else torch.empty(0))
         ctx.has_eid = eid is not None
-        ctx.desc = desc
+        ctx.desc, ctx.bwd = desc, bwd
         return out
 
     @staticmethod
@@ -127,9 +130,8 @@ class _FusedConvFn(torch.autograd.Function):
         gYp = torch.empty(desc.gy_parts, E, 16, dtype=torch.float32, device=X.device) if (ny and E) else None
         gW = torch.empty_like(W) if nw else None
         if E and (nx or ny or nw):
-            getattr(K, f"mm_tpw_{desc.name}_bwd")(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X,
-                                                  X.stride(0), gO, gO.stride(0), gW, W.stride(0), gYp, E * 16, gX,
-                                                  X.stride(0), stream())
+            ctx.bwd(rowptr, n, eid, send, Y, Y.stride(0), W, W.stride(0), X, X.stride(0), gO, gO.stride(0), gW,
+                    W.stride(0), gYp, E * 16, gX, X.stride(0), stream())
         gY = None
         if ny:
             gY = gYp.sum(0) if E else torch.zeros_like(Y)

@@ -1,12 +1,17 @@
 """FusedConvTP (explicit per-edge weights): descriptor and API checks on the CPU; forward and autograd backward of
-the HIP kernels against the fp64 CPU oracle (oracle.mace_ref.channelwise_tp + scatter_sum) on the GPU.
+the HIP kernels against the fp64 CPU oracle (oracle.mace_ref.channelwise_tp + scatter_sum) on the GPU, for the
+library's compiled tables and for tables whose kernels are built at run time (mace_onegpu.tp_jit).
 
 Tolerance (fp32 kernels vs fp64 oracle, sums of <= 353 terms over <= 40 edges): max|d| <= 2e-5 * max|ref|.
 """
+import ctypes
+import os
+
+import numpy as np
 import pytest
 import torch
 
-from mace_onegpu import o3
+from mace_onegpu import o3, tp_jit
 from mace_onegpu.fused_conv import ChannelwiseTP, FusedConvTP
 
 C = 128
@@ -31,7 +36,62 @@ def test_module_api_errors():
     m = FusedConvTP(d, 1280, irreps_out="128x0e+128x1o")
     assert m.weight_numel == 1280 and m.irreps_out == "128x0e+128x1o"
     with pytest.raises(NotImplementedError):
-        ChannelwiseTP([0, 2]).require_kernel()
+        ChannelwiseTP([0, 1], sh_lmax=2).kernels()         # the kernels read 16 harmonics
+    assert "built on first use" in repr(ChannelwiseTP([0, 2]))
+
+
+def test_run_time_tables_are_prebuilt_and_export_their_entry_points():
+    """The build makes the kernels of o3.PREBUILT_JIT_TP_TABLES ahead, from this tree's sources; their libraries
+    load without a GPU and export both entry points under the table's name."""
+    for a, b, c in o3.PREBUILT_JIT_TP_TABLES:
+        desc = ChannelwiseTP(a, b, c)
+        assert desc.name is None
+        assert tp_jit.is_current(desc.table), f"{desc} not built: run __graft_entry__.build()"
+        fwd, bwd = desc.kernels()
+        name = tp_jit.paths(desc.table)[0]
+        assert (fwd.name, bwd.name) == (f"mm_tpw_{name}_fwd", f"mm_tpw_{name}_bwd")
+        assert desc.kernels()[0] is fwd                       # loaded once per process
+
+
+def test_run_time_build_of_a_new_table(tmp_path, monkeypatch):
+    """A table nobody built before: its kernels are generated and compiled on first use (into a scratch directory
+    here), a second request reuses the library, and a library whose recorded source differs is rebuilt."""
+    monkeypatch.setattr(tp_jit, "JIT_DIR", str(tmp_path))
+    t = o3.tp_table([0, 1, 2], 3, (0, 1, 2))
+    assert not tp_jit.is_current(t)
+    so = tp_jit.build(t)
+    assert tp_jit.is_current(t) and os.path.dirname(so) == str(tmp_path)
+    m0 = os.stat(so).st_mtime_ns
+    assert tp_jit.build(t) == so and os.stat(so).st_mtime_ns == m0
+    lib = ctypes.CDLL(so)
+    name = tp_jit.paths(t)[0]
+    for kind in ("fwd", "bwd"):
+        assert getattr(lib, f"mm_tpw_{name}_{kind}")
+    hip = tp_jit.paths(t)[1]
+    with open(hip, "a") as fh:
+        fh.write("// edited\n")
+    assert not tp_jit.is_current(t)
+    tp_jit.build(t)
+    assert tp_jit.is_current(t)
+    assert sorted(os.listdir(tmp_path)) == sorted(os.path.basename(p) for p in tp_jit.paths(t)[1:])
+
+
+@pytest.mark.parametrize("tab", list(o3.PREBUILT_JIT_TP_TABLES) + [((0, 1, 2), 3, (0, 1, 2))])
+def test_sparse_table_matches_the_dense_oracle(tab):
+    """The kernels evaluate the table's sparse terms (w, k, m, o, coef); the oracle contracts the dense coupling
+    tensor of each path.  Both on the CPU in fp64 for a table without a compiled kernel: a wrong component offset,
+    path order or dropped term of the table fails this."""
+    from oracle import mace_ref
+    t = o3.tp_table(list(tab[0]), tab[1], tab[2])
+    g = np.random.default_rng(3)
+    E, Cc = 7, 3
+    W, X, Y = g.normal(size=(E, t["nW"], Cc)), g.normal(size=(E, t["nX"], Cc)), g.normal(size=(E, 16))
+    out = np.zeros((E, t["nO"], Cc))
+    for (w, k, m, o, c) in t["terms"]:
+        out[:, o] += c * W[:, w] * X[:, k] * Y[:, m, None]
+    ref = mace_ref.channelwise_tp(torch.from_numpy(W), torch.from_numpy(X), torch.from_numpy(Y), torch.arange(E),
+                                  t["paths"], t["in_ls"], o3.coupling)
+    np.testing.assert_allclose(out, ref.numpy(), atol=1e-12)
 
 
 def _oracle(desc, X, Y, W, ei, n):
@@ -55,15 +115,11 @@ def _inputs(desc, n, E, seed, sort):
     return X, Y, W, torch.stack([send, recv])
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("in_ls", [[0], [0, 1], [0, 1, 2, 3]])
-@pytest.mark.parametrize("sort", [False, True])
-def test_fused_conv_forward_backward(in_ls, sort):
+def _check(desc, seed, sort):
     assert torch.cuda.is_available(), "GPU test without a GPU"
-    desc = ChannelwiseTP(in_ls)
     n, E = 37, 400
-    X, Y, W, ei = _inputs(desc, n, E, seed=len(in_ls) * 7 + int(sort), sort=sort)
-    print(f"case in_ls={in_ls} sorted={sort} n={n} E={E}", flush=True)
+    X, Y, W, ei = _inputs(desc, n, E, seed=seed, sort=sort)
+    print(f"case {desc} sorted={sort} n={n} E={E}", flush=True)
     Xr, Yr, Wr = (t.clone().requires_grad_(True) for t in (X, Y, W))
     ref = _oracle(desc, Xr, Yr, Wr, ei, n)
     R = torch.randn(ref.shape, generator=torch.Generator().manual_seed(5), dtype=torch.float64)
@@ -78,6 +134,23 @@ def test_fused_conv_forward_backward(in_ls, sort):
         print(f"  {name}: max|d| {err:.3e} (max|ref| {scale:.3e})", flush=True)
         assert err <= 2e-5 * scale, name
     assert float(out.detach()[n - 3:].abs().max()) == 0.0       # rows of nodes without edges
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("in_ls", [[0], [0, 1], [0, 1, 2, 3]])
+@pytest.mark.parametrize("sort", [False, True])
+def test_fused_conv_forward_backward(in_ls, sort):
+    _check(ChannelwiseTP(in_ls), len(in_ls) * 7 + int(sort), sort)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tab", o3.PREBUILT_JIT_TP_TABLES)
+@pytest.mark.parametrize("sort", [False, True])
+def test_fused_conv_run_time_tables(tab, sort):
+    """Tables whose kernels are built at run time (made ahead by the build, so nothing compiles here)."""
+    desc = ChannelwiseTP(*tab)
+    assert desc.name is None and tp_jit.is_current(desc.table)
+    _check(desc, 100 + len(tab[0]) * 7 + len(tab[2]) + int(sort), sort)
 
 
 @pytest.mark.gpu
