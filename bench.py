@@ -96,6 +96,11 @@ KERNEL_SOURCES = {
     "mm_conv2_fwd_kernel": ("gen/conv_l2.hip", "gen/sh.h", "common.h"),
     "mm_ace1_fwd_kernel": ("ace.hip", "gen/sh.h", "common.h"),
     "mm_ace1_bwd_kernel": ("ace.hip", "gen/sh.h", "common.h"),
+    "mm_conv1_fwd_kernel": ("gen/conv_l1.hip", "gen/sh.h", "common.h"),
+    "mm_conv1_bwd_kernel": ("gen/conv_l1.hip", "gen/sh.h", "common.h"),
+    "mm_conv0123_fwd_kernel": ("gen/conv_l0123.hip", "gen/sh.h", "common.h"),
+    "mm_conv0123_bwd_kernel": ("gen/conv_l0123.hip", "gen/sh.h", "common.h"),
+    **{f"mm_tpw_{t}_{d}_kernel": (f"gen/tpw_{t}.hip", "common.h") for t in ("l1", "l2", "l0123") for d in ("fwd", "bwd")},
     "mm_linear_kernel": ("linear.hip", "common.h"),
     "mm_fill_f32_kernel": ("node.hip", "common.h"),
     "mm_fill_i32_kernel_nl": ("nlist.hip", "common.h"),
@@ -117,7 +122,8 @@ def kernel_digest(kernel, read=None):
     return h.hexdigest()
 
 
-TRAFFIC_FILES = ("traffic_config5_water1M.json", "traffic_config3_water98k.json", "traffic_config4_fcc500k.json")
+TRAFFIC_FILES = ("traffic_config5_water1M.json", "traffic_config3_water98k.json", "traffic_config4_fcc500k.json",
+                 "traffic_config2_chunk16k.json")
 
 
 def measured_traffic(kernel, workload):
@@ -809,8 +815,10 @@ def run_conv(a):
                      {"workload": "config2: edge-convolution kernels on chunk 0 (16,384 receivers) of the 98,304-atom "
                                   "water box", "edges": E, "receivers": nC, "nodes": nN,
                       "check_vs_FusedConvTP_max_rel": err, "check_vs_oracle": oracle_check},
-                     roofline_of(kernels), kernels, cpu)
+                     roofline_of(kernels, {"config": 2, "chunk": 16384}), kernels, cpu)
     line["steps_note"] = "steps = launches of each kernel"
+    if a.copy_calib_mib > 0:
+        copy_calibration(a.copy_calib_mib)
     return line
 
 
