@@ -72,7 +72,8 @@ int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] *
  * e_u float4 (unit vector, length; the convolutions and the ACE kernels evaluate Y_lm l<=3 from it), optionally
  * the 16 harmonics e_Y (nullable; the production path passes null), the local receiver, and a packed
  * float4 (t, spline interval row of the ordered species pair's table, sender feature row (its species when
- * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r).  dens_w is HOST [nb].  E_dev (nullable): the edge
+ * x_from_spec), edge density tanh((B . w)^2) f_cut), plus d'(r); t = -0 marks a length below r_lo, where W is
+ * W(r_lo) and the backward kernels take its r-derivative as zero.  dens_w is HOST [nb].  E_dev (nullable): the edge
  * count read from device memory instead of E, which then only sizes the launch (E_dev <= E; a captured HIP graph
  * replays a chunk's real count with the grid of its capacity). */
 int mm_edge_geom_rij(int E, const int* E_dev /* nullable */, const double* rij, const int* pair_i, int a,

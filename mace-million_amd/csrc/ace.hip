@@ -422,7 +422,7 @@ mm_ace1_bwd_kernel(const int* __restrict__ rowptr, int nC, const floatx4* __rest
         const int sl = tb + 4 * g + v;
         const int ej = __float_as_int(rec[sl].z);
         const float yv = ej >= 0 ? yt[(4 * g + v) * 16 + i16] : 0.f;
-        sgr[v] = mm_row_sum16(dYp[v] * yv) * inv_h;
+        sgr[v] = mm_row_sum16(dYp[v] * yv) * mm_spline_dxdr(rec[sl].x, inv_h);
         sev[v] = ej >= 0 ? sb + ej : -1;
       }
       sdY = dY;

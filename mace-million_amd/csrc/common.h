@@ -43,6 +43,13 @@ __device__ __forceinline__ int mm_xcd_channel_block() {
   return blockIdx.x & (MM_NCB - 1);
 }
 
+// dx/dr of an edge's spline coordinate x = (r - r_lo) / h: inv_h inside the table; zero for a length below the
+// table start, which the geometry kernels mark with t = -0 (x clamped to 0, so W is W(r_lo) and does not vary with
+// r there: a zero derivative keeps the forces the derivative of the energy that the forward evaluates).
+__device__ __forceinline__ float mm_spline_dxdr(float t, float inv_h) {
+  return __float_as_int(t) < 0 ? 0.f : inv_h;
+}
+
 // DPP (data-parallel primitive) lane moves inside a row of 16 lanes; used for channel reductions without LDS.
 template <int CTRL>
 __device__ __forceinline__ float mm_dpp(float v) {

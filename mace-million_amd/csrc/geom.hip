@@ -63,6 +63,9 @@ __device__ __forceinline__ void mm_density(float r, const MMDensity& dp, float& 
 // (the clamp of spline_w._coords, spline_w.py:18-27).  The tables hold M - 1 intervals, so k is also clamped to
 // M - 2: for M >= 4096 the fp32 value M - 1 - 1e-4 rounds to M - 1, and floor(x) alone would index one interval
 // past the table (then t = x - k = 1, the right end of the last interval).
+// A length below r_lo gets t = -0: W is W(r_lo) there (the same value as t = +0), and the backward kernels read
+// the sign as "dx/dr = 0" (mm_spline_dxdr).  The reference's backward takes the table's slope at the clamped end
+// (spline_w.py:63-79), a force that is not the derivative of its energy there.
 struct MMSpline {
   int M;
   float r_lo, inv_h;
@@ -87,14 +90,16 @@ __device__ __forceinline__ void mm_geom_common(int e, float vx, float vy, float 
     yp[3] = make_float4(Y[12], Y[13], Y[14], Y[15]);
   }
   const int tab = pair_map[node_spec[send] * S + node_spec[recv]];
-  const float x = fminf(fmaxf((r - sp.r_lo) * sp.inv_h, 0.f), (float)(sp.M - 1) - 1e-4f);
+  const float xr = (r - sp.r_lo) * sp.inv_h;
+  const float x = fminf(fmaxf(xr, 0.f), (float)(sp.M - 1) - 1e-4f);
   const float kf = fminf(floorf(x), (float)(sp.M - 2));
   const int row = tab * (sp.M - 1) + (int)kf;
+  const float t = xr < 0.f ? -0.f : x - kf;
   const int xsrc = x_from_spec ? node_spec[send] : send;
   e_recv[e] = recv;
   float d, dd;
   mm_density(r, dp, d, dd);
-  e_pk[e] = make_float4(x - kf, __int_as_float(row), __int_as_float(xsrc), d);
+  e_pk[e] = make_float4(t, __int_as_float(row), __int_as_float(xsrc), d);
   e_dd[e] = dd;
 }
 

@@ -3,11 +3,13 @@
 Semantics checked (fast_layers.py:154-156, 179-183, 190-192; spline_w._coords, spline_w.py:18-27):
     e_u[e]  = (v / |v|, |v|),  v = rij[e] rounded to fp32 (rij.to(dtype), mliap_threepass.py:326)
     e_pk[e] = (t, table(pair) * (M - 1) + k, sender feature row, d(|v|)),  x = clamp((r - r_lo) / h, 0, M - 1 - 1e-4),
-              k = floor(x), t = x - k, pair = (species(send), species(recv)), d(r) = tanh((B(r) . w)^2) f_cut(r)
+              k = floor(x), t = x - k (t = -0 below r_lo), pair = (species(send), species(recv)),
+              d(r) = tanh((B(r) . w)^2) f_cut(r)
     e_dd[e] = d'(r),  e_recv[e] = pair_i[e] - a
 Lengths are drawn away from the knots (t in [0.05, 0.95]) so that the interval is the same in fp32 and fp64.
 """
 import ctypes
+import math
 
 import pytest
 import torch
@@ -123,3 +125,5 @@ def test_spline_interval_stays_inside_the_table(M):
     assert row[:5].tolist() == [M - 2] * 5                        # r >= r_max - h/2: the last interval
     assert row[5:].tolist() == [0, 0]                             # r <= r_lo + h/4: the first interval
     assert float(t[6]) == 0.0                                     # below r_lo: clamped to the first knot
+    # a length below r_lo is marked by the sign of t = -0 (its spline derivative is zero); r_lo + h/4 is not
+    assert math.copysign(1.0, float(t[6])) == -1.0 and math.copysign(1.0, float(t[5])) == 1.0

@@ -339,6 +339,46 @@ def test_replica_and_translation_at_size(dev, model):
     assert float((F2o - F_orig).abs().max()) < 1e-5 * float(F.abs().max())
 
 
+def test_forces_are_the_energy_gradient_below_the_table_start(dev, model):
+    """A pair closer than the spline tables' first knot (r_lo = 0.5 A; such pairs occur by the tens of thousands
+    in configuration 5's MD with this random-weight model, which has no short-range repulsion).  Below r_lo the
+    radial weights are clamped to W(r_lo) (the clamp of spline_w._coords, spline_w.py:18-27), so the forces must
+    leave out their r-derivative there; the reference's backward takes the table's slope at the clamped end
+    instead, which made the full-size MD gain 318 eV over 100 steps.  The H atom of molecule 1 is put 0.3 A from
+    the O atom of molecule 0, and its force is compared with a 4-point central difference of the total energy
+    (h = 1e-3 A along x, y and z; both atoms stay below r_lo).  Measured: 1.2e-5 eV/A, and 3.0e-2 eV/A with the
+    slope taken as the reference takes it; the bound, 2e-4 eV/A, lies between them (the difference's fp32 noise
+    is about 1e-8 eV of energy over 1e-3 A)."""
+    from mace_onegpu import systems
+    from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE, System
+    pos, box, Z = systems.water_box(64, seed=3)
+    pos = pos.copy()
+    u = np.array([0.48, -0.6, 0.64])
+    pos[4] = pos[0] + 0.3 * u / np.linalg.norm(u)
+
+    def energy_forces(p):
+        s = System(p, box, Z - 1, 6.0, dev)
+        s.build_neighbors()
+        E, eat, F, PF = ReceiverChunkMACE(model, chunk=4096, device=dev).compute(s)
+        Fo = torch.empty_like(F)
+        Fo[s.perm.long()] = F
+        return E, Fo.cpu().numpy()
+
+    E0, F0 = energy_forces(pos)
+    h = 1e-3
+    fd = np.zeros(3)
+    for d in range(3):
+        e = {}
+        for k in (1, -1, 2, -2):
+            p = pos.copy()
+            p[4, d] += k * h
+            e[k] = energy_forces(p)[0]
+        fd[d] = -(8 * (e[1] - e[-1]) - (e[2] - e[-2])) / (12 * h)
+    err = float(np.abs(fd - F0[4]).max())
+    _say(f"  pair at 0.3 A: F {F0[4].tolist()}  F_fd {fd.tolist()}  max|F - F_fd| {err:.3e} eV/A")
+    assert err < 2e-4
+
+
 def test_md_steps_conserve_energy(dev, model):
     """Ten velocity-Verlet steps of a 1,536-atom box: the skin-filtered pair list equals a fresh build and the
     total energy drift stays far below the kinetic energy."""

@@ -13,6 +13,8 @@ ReceiverChunkMACE at the production chunk of 131,072 receivers (about 11.8 M edg
   chunk.
 * Configuration 4 (500,000-atom FCC, four species) at full size: per-atom energies against the oracle and a
   finite-difference force.
+* Configuration 5's MD protocol in full (100 velocity-Verlet steps of 0.5 fs from 300 K, HIP-graph chunks, skin
+  list rebuilt on displacement): the first energy equals the base box's, and the total energy is conserved.
 """
 import numpy as np
 import pytest
@@ -161,3 +163,43 @@ def test_config4_per_atom_energies_and_forces_at_full_size(model, ref_model):
     err = float(np.abs(np.array(fd) - F0[i].numpy()).max())
     _say(f"  atom {i} (Z {Z[i]}): F {F0[i].tolist()}  F_fd {fd}; max|F - F_fd| {err:.3e} eV/A")
     assert err < 5e-5
+
+
+def test_config5_md_100_steps_conserve_energy(model, water_config5, base5):
+    """The reference's configuration-5 run (343,000 molecules, 100 steps of 0.5 fs, Maxwell-Boltzmann 300 K with
+    seed 4, neighbour list at r_max + 2 A rebuilt when an atom has moved 1 A) through MDRunner with HIP-graph
+    chunks at chunk 131072, as the bench runs it.  The first evaluation has the base box's energy per atom (another
+    atom order and other chunks: fp32 rounding, as in the replica test), the skin list is rebuilt at least once,
+    and E_pot + E_kin stays constant: velocity Verlet's energy error at this step is O(dt^2) and bounded.  The
+    bounds: 1e-4 of the kinetic energy (4 eV of 4.0e4 eV), and 2 % of the range of E_pot over the run, which the
+    forces' work must balance (a force term that is missing, mis-signed or off by a few per cent leaves a drift of
+    that order)."""
+    from mace_onegpu.md import MDRunner
+    pos, box, Z = water_config5
+    E0 = base5[0]
+    N = len(pos)
+    _say("case config5 MD: 100 steps of 0.5 fs, HIP-graph chunks")
+    md = MDRunner(model, pos, box, Z, chunk=CHUNK, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device="cuda",
+                  use_graphs=True)
+    md.forces()
+    dE0 = abs(md.E - E0) / N
+    e_pot, e_kin = [md.E], [md.kinetic()]
+    for k in range(100):
+        md.step()
+        e_pot.append(md.E)
+        e_kin.append(md.kinetic())
+        if k % 20 == 19:
+            _say(f"  step {k + 1}: E_pot {md.E:.6f} E_kin {e_kin[-1]:.6f} E_tot {md.E + e_kin[-1]:.6f} "
+                 f"rebuilds {md.n_rebuild}")
+    e_tot = np.array(e_pot) + np.array(e_kin)
+    drift = float(e_tot.max() - e_tot.min())
+    work = float(np.abs(np.diff(e_pot)).sum())
+    _say(f"  |dE/N| at step 0 {dE0:.3e} eV; E_tot range {drift:.3e} eV over 100 steps (E_kin {e_kin[-1]:.1f} eV, "
+         f"E_pot range {float(np.ptp(e_pot)):.3e} eV, sum |dE_pot| {work:.3e} eV), {md.n_rebuild} builds")
+    builds = md.n_rebuild
+    del md
+    torch.cuda.empty_cache()
+    assert dE0 < 1e-9
+    assert builds >= 2
+    assert drift < 1e-4 * e_kin[-1]
+    assert drift < 0.02 * float(np.ptp(e_pot))
