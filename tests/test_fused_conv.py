@@ -53,6 +53,18 @@ def test_run_time_tables_are_prebuilt_and_export_their_entry_points():
         assert desc.kernels()[0] is fwd                       # loaded once per process
 
 
+def test_run_time_kernels_report_their_own_errors():
+    """An argument error of a run-time library's entry point is raised with that library's message (its own
+    mm_last_error), checked on the host before anything reaches the GPU."""
+    desc = ChannelwiseTP(*o3.PREBUILT_JIT_TP_TABLES[0])
+    fwd, bwd = desc.kernels()
+    with pytest.raises(RuntimeError, match="row strides smaller than the path table's widths"):
+        fwd(None, 1, None, None, None, 8, None, desc.nW * C, None, desc.nX * C, None, desc.nO * C, None)
+    with pytest.raises(RuntimeError, match="bad sizes"):
+        bwd(None, -1, None, None, None, 16, None, desc.nW * C, None, desc.nX * C, None, desc.nO * C, None, 0, None, 0,
+            None, 0, None)
+
+
 def test_run_time_build_of_a_new_table(tmp_path, monkeypatch):
     """A table nobody built before: its kernels are generated and compiled on first use (into a scratch directory
     here), a second request reuses the library, and a library whose recorded source differs is rebuilt."""
