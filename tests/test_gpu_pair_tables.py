@@ -75,3 +75,24 @@ def test_pair_tables_mliap_graphs(pair_setup, monkeypatch):
         eat = data.eatoms
         _check("vs oracle, same tables", data.energy, eat, data.atom_forces(), ref_tab, s.N, 2e-5)
     assert tp._rt.gx is not None and tp._rt.gx.n_replays > 0 and tp._rt.fl.n_tab == 3
+
+
+def test_pair_tables_md_conserves_energy(pair_setup):
+    """Velocity Verlet with the per-pair model (the layer-1 convolution with 3 tables) on a 12,288-atom water box,
+    50 steps of 0.5 fs from 300 K with HIP-graph chunks: E_pot + E_kin stays within 1 % of the range of E_pot
+    (measured: 3.6e-3 eV against 8.8 eV)."""
+    from mace_onegpu import systems
+    from mace_onegpu.md import MDRunner
+    m = pair_setup[0]
+    pos, box, Z = systems.water_box(4096, seed=0)
+    md = MDRunner(m, pos, box, Z, chunk=4096, skin=2.0, dt_fs=0.5, T=300.0, seed_v=4, device="cuda",
+                  use_graphs=True)
+    md.forces()
+    e_pot, e_kin = [md.E], [md.kinetic()]
+    for _ in range(50):
+        md.step()
+        e_pot.append(md.E)
+        e_kin.append(md.kinetic())
+    drift = float(np.ptp(np.array(e_pot) + np.array(e_kin)))
+    _say(f"  pair-table MD: E_tot range {drift:.3e} eV, E_pot range {float(np.ptp(e_pot)):.3e} eV")
+    assert drift < 0.01 * float(np.ptp(e_pot))
