@@ -117,6 +117,51 @@ def test_mliap_graphs_vs_oracle(dev, scaled_model, scaled_ref, water, cache_l1, 
     assert tp._rt.gx is not None and tp._rt.gx.n_replays == 24 and tp.n_captures == 1
 
 
+@pytest.mark.parametrize("graphs", ["0", "1"])
+def test_mliap_md_conserves_energy(dev, scaled_model, graphs, monkeypatch):
+    """LAMMPS' side of an MD run through the plugin: every step builds the periodic-image data object anew from the
+    moved atoms (new ghosts, owners and pair order) and calls compute_forces, and the host integrates with velocity
+    Verlet (0.5 fs, 300 K, 30 steps, 1,536 water atoms; chunks of 512, replayed from HIP graphs with
+    MACE3P_GRAPHS=1).  E_pot + E_kin stays within 1 % of the range of E_pot over the run (measured: 2.2e-3 eV
+    against 0.89 eV, eager and with graphs): the plugin's pair forces, summed per atom through pair_i / pair_j and
+    the ghosts' owners, are the energy's derivative."""
+    from mace_onegpu import systems
+    from mace_onegpu.lammps_data import PeriodicMLIAPData
+    from mace_onegpu.md import ACC
+    from mace_onegpu.mliap_threepass import ThreePassMLIAP
+    from mace_onegpu.receiver_chunk_mace import System
+    monkeypatch.setenv("MACE3P_GRAPHS", graphs)
+    pos, box, Z = systems.water_box(512, seed=1)
+    vel, mass = systems.maxwell_boltzmann(Z, 300.0, 4)
+    tp = ThreePassMLIAP(scaled_model, chunk=512)
+
+    def energy_forces(p):
+        s = System(p, box, Z - 1, 6.0, dev)
+        s.build_neighbors()
+        data = PeriodicMLIAPData(s, s.spidx.long(), ghosts=True)
+        tp.compute_forces(data)
+        F = torch.empty(s.N, 3, dtype=torch.float64, device=dev)
+        F[s.perm.long()] = data.atom_forces()
+        return data.energy, F.cpu().numpy()
+
+    dt = 0.5e-3
+    E, F = energy_forces(pos)
+    e_pot, e_kin = [E], [0.5 * float((mass[:, None] * vel ** 2).sum()) / ACC]
+    for _ in range(30):
+        vel = vel + 0.5 * dt * F / mass[:, None] * ACC
+        pos = pos + dt * vel
+        E, F = energy_forces(pos)
+        vel = vel + 0.5 * dt * F / mass[:, None] * ACC
+        e_pot.append(E)
+        e_kin.append(0.5 * float((mass[:, None] * vel ** 2).sum()) / ACC)
+    drift = float(np.ptp(np.array(e_pot) + np.array(e_kin)))
+    _say(f"  plugin MD graphs={graphs}: E_tot range {drift:.3e} eV, E_pot range {float(np.ptp(e_pot)):.3e} eV, "
+         f"E_kin {e_kin[-1]:.2f} eV")
+    if graphs == "1":
+        assert tp.n_captures >= 1
+    assert drift < 0.01 * float(np.ptp(e_pot))
+
+
 def test_standalone_graphs_vs_oracle(dev, scaled_model, scaled_ref, water):
     """ReceiverChunkMACE(use_graphs=True): three full chunks of 64 receivers, two calls."""
     from mace_onegpu.receiver_chunk_mace import ReceiverChunkMACE
