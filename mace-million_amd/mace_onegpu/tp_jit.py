@@ -5,7 +5,8 @@ the irreps at run time (fused_edge_conv.py:43-68), as conv_spline generates its 
 (conv_spline.py:38-181).  The library here carries the tables of o3.COMPILED_TP_TABLES.  For any other table
 (spherical harmonics up to l = 3) this module generates the same straight-line kernels (codegen.tpw_source) and
 builds them with the library's own compiler flags into a small shared library next to it,
-lib/jit/tpw_j<key>.so (key: a hash of the table), the first time the table is used; later calls and processes load
+lib/jit/tpw_j<key>.so (key: a hash of the table; MM_TP_JIT_DIR names another directory), the first time the
+table is used; later calls and processes load
 the built file.  A file built from other sources (another generator, common.h or api.cpp) is rebuilt.  Building
 takes seconds to a minute and needs hipcc; build.py builds the tables of o3.PREBUILT_JIT_TP_TABLES ahead.
 """
@@ -23,7 +24,8 @@ from ._lib import I, L, P, _Fn
 
 PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))     # mace-million_amd/
 CSRC = os.path.join(PKG, "csrc")
-JIT_DIR = os.path.join(PKG, "lib", "jit")
+# where the run-time libraries live: next to the library, or MM_TP_JIT_DIR (e.g. for a read-only install)
+JIT_DIR = os.environ.get("MM_TP_JIT_DIR") or os.path.join(PKG, "lib", "jit")
 
 # argument types of mm_tpw_<name>_fwd / _bwd (include/mace_million_amd.h)
 SIG_FWD = [P, I, P, P, P, L, P, L, P, L, P, L, P]
