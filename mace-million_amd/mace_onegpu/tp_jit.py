@@ -4,11 +4,10 @@ The reference's FusedConvTP evaluates any channelwise path table: cuEquivariance
 the irreps at run time (fused_edge_conv.py:43-68), as conv_spline generates its Triton kernels for a table
 (conv_spline.py:38-181).  The library here carries the tables of o3.COMPILED_TP_TABLES.  For any other table
 (spherical harmonics up to l = 3) this module generates the same straight-line kernels (codegen.tpw_source) and
-builds them with the library's own compiler flags into a small shared library next to it,
-lib/jit/tpw_j<key>.so (key: a hash of the table; MM_TP_JIT_DIR names another directory), the first time the
-table is used; later calls and processes load
-the built file.  A file built from other sources (another generator, common.h or api.cpp) is rebuilt.  Building
-takes seconds to a minute and needs hipcc; build.py builds the tables of o3.PREBUILT_JIT_TP_TABLES ahead.
+builds them with the library's own compiler flags into a small shared library next to it, lib/jit/tpw_j<key>.so
+(key: a hash of the table; MM_TP_JIT_DIR names another directory), the first time the table is used; later calls
+and processes load the built file.  A file built from other sources (another generator, common.h or api.cpp) is
+rebuilt.  Building takes about 5 s and needs hipcc; build.py builds the tables of o3.PREBUILT_JIT_TP_TABLES ahead.
 """
 import ctypes
 import hashlib
