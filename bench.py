@@ -891,16 +891,6 @@ def symc_gemm_probe():
                       "bmm_fp32_16col_TFLOPs": round(res[16][1], 2)}), flush=True)
 
 
-def replicate(pos, box, Z, reps):
-    """Periodic replica (nx, ny, nz) of a box: copy c = (ix, iy, iz) (ix slowest) holds atoms c * N .. c * N + N - 1
-    at pos + (ix, iy, iz) * box, so atom j of the replica is atom j % N of the base box."""
-    import numpy as np
-    nx, ny, nz = reps
-    sh = np.array([(ix, iy, iz) for ix in range(nx) for iy in range(ny) for iz in range(nz)], dtype=np.float64)
-    pos_r = (pos[None, :, :] + (sh * np.asarray(box))[:, None, :]).reshape(-1, 3)
-    return pos_r, np.asarray(box) * np.array(reps, dtype=np.float64), np.tile(Z, len(sh))
-
-
 def run_capacity(a):
     """Memory and exactness at scale: the configuration-5 water box and its periodic replicas evaluated by
     ReceiverChunkMACE (chunk 131072, eager chunks) in three memory layouts: the default one with the pass-A
@@ -923,7 +913,7 @@ def run_capacity(a):
 
     def one(rp, mode, rec):
         n_rep = rp[0] * rp[1] * rp[2]
-        p_r, b_r, z_r = replicate(pos, box, Z, rp) if n_rep > 1 else (pos, box, Z)
+        p_r, b_r, z_r = systems.replicate(pos, box, Z, rp) if n_rep > 1 else (pos, box, Z)
         rec["atoms"] = len(p_r)
         s = System(p_r, b_r, z_r - 1, 6.0, "cuda")
         s.build_neighbors()

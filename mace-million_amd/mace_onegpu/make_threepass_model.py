@@ -18,17 +18,7 @@ import argparse
 import torch
 
 from .mliap_threepass import ThreePassMLIAP
-from .model import MaceModel, MaceSpec
-
-
-def load_weights(model, path):
-    if path.endswith(".safetensors"):
-        from safetensors.torch import load_file
-        sd = load_file(path)
-    else:
-        sd = torch.load(path, map_location="cpu", weights_only=True)
-    model.load_state_dict(sd, strict=True)
-    return model
+from .model import MaceModel, MaceSpec, load_weights
 
 
 def make(out, seed=0, weights=None, chunk=16384, spline_grid=512, recipe=False):

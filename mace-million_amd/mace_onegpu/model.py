@@ -157,3 +157,22 @@ class MaceModel(torch.nn.Module):
 
     def forward(self, *a, **k):   # pragma: no cover - the model is evaluated by the three-pass path only
         raise RuntimeError("MaceModel holds parameters; evaluate it with ThreePassMLIAP or ReceiverChunkMACE")
+
+
+def load_weights(model, path):
+    """Loads a state_dict (safetensors, or a weights-only torch file) into the model, every parameter required."""
+    if path.endswith(".safetensors"):
+        from safetensors.torch import load_file
+        sd = load_file(path)
+    else:
+        sd = torch.load(path, map_location="cpu", weights_only=True)
+    model.load_state_dict(sd, strict=True)
+    return model
+
+
+def from_arg(arg):
+    """The --model option of the command-line entry points: "seed:N" gives the random-init architecture with seed
+    N; anything else names a weights file for it (load_weights)."""
+    if arg.startswith("seed:"):
+        return MaceModel(seed=int(arg[5:]))
+    return load_weights(MaceModel(seed=0), arg)

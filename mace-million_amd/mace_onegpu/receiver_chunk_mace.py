@@ -410,3 +410,97 @@ def pair_to_atom_forces(sysm, PF, graphs=None):
     F = torch.empty(N, 3, dtype=torch.float64, device=dev)
     K.mm_pair_forces_to_atoms(N, sysm.rowptr, sysm._s_rowptr, sysm._s_perm, PF, F, stream())
     return F
+
+
+def _sync():
+    torch.cuda.synchronize()
+
+
+def _in_input_order(sysm, t):
+    """Rows of a sorted-index-space tensor in the input atom order (sysm.perm: sorted -> input index)."""
+    out = torch.empty_like(t)
+    out[sysm.perm.long()] = t
+    return out
+
+
+def main(argv=None):
+    """Command line of the standalone evaluator (the reference's receiver_chunk_mace.main, :422-518): energy and
+    forces of one structure, with the neighbour-list and evaluation times, peak device memory and, optionally, the
+    replica check (every atom of a periodic replica against its image in the base cell, evaluated alone) and a
+    JSON record.
+
+        python -m mace_onegpu.receiver_chunk_mace --water 343000 --chunk 131072 --repeat 3 --graphs
+        python -m mace_onegpu.receiver_chunk_mace --base cell.xyz --rep 4 4 4 --check-replica --json out.json
+    """
+    import argparse
+    import json
+
+    from . import systems
+    from .model import from_arg
+
+    ap = argparse.ArgumentParser(prog="python -m mace_onegpu.receiver_chunk_mace", description=main.__doc__.split(
+        "\n\n")[0])
+    ap.add_argument("--model", default="seed:0", help='"seed:N" (random-init weights) or a weights file '
+                                                      "(.safetensors or a weights-only torch state_dict)")
+    systems.add_structure_args(ap)
+    ap.add_argument("--chunk", type=int, default=131072, help="receivers per chunk")
+    ap.add_argument("--repeat", type=int, default=1, help="evaluations of the same structure")
+    ap.add_argument("--graphs", action="store_true", help="replay full chunks from HIP graphs")
+    ap.add_argument("--low-memory", action="store_true", help="the reference's memory layout (per-pass topologies)")
+    ap.add_argument("--deterministic", action="store_true", help="bitwise-repeatable sender-feature gradient")
+    ap.add_argument("--check-replica", action="store_true", help="with --rep: every atom against its base image")
+    ap.add_argument("--json", default=None, help="write the results here")
+    a = ap.parse_args(argv)
+    if a.check_replica and tuple(a.rep) == (1, 1, 1):
+        ap.error("--check-replica needs --rep with more than one copy")
+    if not torch.cuda.is_available():
+        raise SystemExit("the evaluator runs on the GPU; no GPU is visible")
+    model = from_arg(a.model)
+    r_max = float(model.spec.r_max)
+    pos, box, Z, base = systems.structure_from_args(a)
+    N = len(pos)
+    print(f"N={N:,} box={np.round(box, 3).tolist()} chunk={a.chunk} graphs={a.graphs} low_memory={a.low_memory} "
+          f"model={a.model}", flush=True)
+    t0 = time.perf_counter()
+    s = System(pos, box, np.asarray(Z) - 1, r_max, "cuda")
+    s.build_neighbors()
+    _sync()
+    n_pairs = int(s.rowptr[-1])
+    res = dict(N=N, pairs=n_pairs, chunk=a.chunk, graphs=a.graphs, low_memory=a.low_memory, model=a.model,
+               t_neighbours=time.perf_counter() - t0, runs=[])
+    print(f"neighbour list: {n_pairs:,} pairs ({n_pairs / N:.2f} per atom), {res['t_neighbours']:.2f} s", flush=True)
+    ev = ReceiverChunkMACE(model, chunk=a.chunk, device="cuda", use_graphs=a.graphs, low_memory=a.low_memory,
+                           deterministic=True if a.deterministic else None)
+    E = eat = F = None
+    for rep in range(a.repeat):
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        E, eat, F, _ = ev.compute(s)
+        _sync()
+        tt = time.perf_counter() - t0
+        peak = torch.cuda.max_memory_allocated() / 1e9
+        res["runs"].append(dict(energy=E, t_total=tt, atom_step_per_s=N / tt, peak_gb=peak))
+        print(f"[rep {rep}] E={E:.6f} eV  t={tt:.3f} s ({N / tt:.3e} atom-step/s)  peak={peak:.2f} GB", flush=True)
+    if a.check_replica:
+        pb, bb, zb = base
+        nb = len(pb)
+        sb = System(pb, bb, np.asarray(zb) - 1, r_max, "cuda")
+        sb.build_neighbors()
+        Eb, eb, Fb, _ = ReceiverChunkMACE(model, chunk=a.chunk, device="cuda").compute(sb)
+        Fb, eb = _in_input_order(sb, Fb), _in_input_order(sb, eb)
+        Fo, eo = _in_input_order(s, F), _in_input_order(s, eat)
+        img = torch.arange(N, device=Fo.device) % nb
+        dF = float((Fo - Fb[img]).abs().max())
+        de = float((eo - eb[img]).abs().max())
+        res["replica_check"] = dict(base_atoms=nb, max_dF=dF, max_de=de, dE_per_atom=E / N - Eb / nb,
+                                    max_F=float(Fb.abs().max()))
+        print(f"REPLICA CHECK against the {nb}-atom base cell, every one of {N:,} atoms: max|dF|={dF:.3e} eV/A  "
+              f"max|de_i|={de:.3e} eV  E/N - E_base/N_base = {E / N - Eb / nb:+.3e} eV/atom", flush=True)
+    if a.json:
+        with open(a.json, "w") as fh:
+            json.dump(res, fh, indent=1)
+    return res
+
+
+if __name__ == "__main__":
+    main()
