@@ -78,6 +78,16 @@ def test_codegen_term_coverage():
     assert len(re.findall(r"acc\d+ = fmaf\(", fwd1)) == len(t.tp1["terms"])
 
 
+def test_codegen_rejects_a_batch_that_is_not_a_power_of_two():
+    """The forward's per-edge batch is found with masks: 48 would mix two batches' rows (results wrong, no fault)."""
+    from mace_onegpu import codegen, model
+    t = model.Tables(model.MaceSpec())
+    for yb in (48, 128, 2):
+        with pytest.raises(ValueError, match="power of two"):
+            codegen.conv_source(t.tp2, 2, True, {"ybatch": yb})
+    assert "yf_all[4 * 480]" in codegen.conv_source(t.tp2, 2, True, {"ybatch": 32})
+
+
 @pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (python mace-million_amd/build.py)")
 def test_readout1_refuses_half_gradient_mode():
     """mm_readout1 computes energies only when g1r and gh are both null and the gradient when both are given; one
