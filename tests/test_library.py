@@ -86,6 +86,8 @@ def test_codegen_rejects_a_batch_that_is_not_a_power_of_two():
         with pytest.raises(ValueError, match="power of two"):
             codegen.conv_source(t.tp2, 2, True, {"ybatch": yb})
     assert "yf_all[4 * 480]" in codegen.conv_source(t.tp2, 2, True, {"ybatch": 32})
+    with pytest.raises(ValueError, match="cpl"):
+        codegen.conv_source(t.tp2, 2, True, {"cpl": 3})
 
 
 @pytest.mark.skipif(not os.path.exists(LIB), reason="library not built (python mace-million_amd/build.py)")
