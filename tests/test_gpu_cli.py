@@ -10,16 +10,16 @@ pytestmark = pytest.mark.gpu
 
 
 def test_evaluator_replica_check_and_record(tmp_path):
-    """python -m mace_onegpu.receiver_chunk_mace --water 64 --rep 2 2 2 --check-replica --graphs --repeat 2: every
-    atom of the 1,536-atom replica has its base image's force and energy (fp32 arithmetic in other orders), and
-    the record holds both runs."""
+    """python -m mace_onegpu.receiver_chunk_mace --water 64 --rep 3 2 1 --check-replica --graphs --repeat 2: every
+    atom of the 1,152-atom replica (a box of 3 x 2 x 1 base cells: cell grids of three different lengths) has its
+    base image's force and energy (fp32 arithmetic in other orders), and the record holds both runs."""
     from mace_onegpu.receiver_chunk_mace import main
     assert torch.cuda.is_available(), "GPU test without a GPU"
     out = tmp_path / "r.json"
-    res = main(["--water", "64", "--rep", "2", "2", "2", "--chunk", "256", "--graphs", "--repeat", "2",
+    res = main(["--water", "64", "--rep", "3", "2", "1", "--chunk", "256", "--graphs", "--repeat", "2",
                 "--check-replica", "--json", str(out)])
     rc = res["replica_check"]
-    assert res["N"] == 1536 and res["pairs"] > 0 and len(res["runs"]) == 2
+    assert res["N"] == 1152 and res["pairs"] > 0 and len(res["runs"]) == 2
     assert rc["max_dF"] < 1e-5 * rc["max_F"] and rc["max_de"] < 1e-6 and abs(rc["dE_per_atom"]) < 1e-9
     assert res["runs"][0]["energy"] == pytest.approx(res["runs"][1]["energy"], abs=1e-9)
     assert json.loads(out.read_text())["replica_check"] == rc
