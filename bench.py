@@ -509,6 +509,7 @@ def run_md(a):
         md.step()
         print(f"# warmup step {i}: E/N {md.E / N:.6f} eV", file=sys.stderr, flush=True)
     rebuilds0 = md.n_rebuild
+    e_tot0 = md.E + md.kinetic()          # total energy before and after the timed steps (outside the timing)
     fl = md.ev.fl
     fl.start_kernel_timing()
     torch.cuda.synchronize()
@@ -518,6 +519,8 @@ def run_md(a):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ktimes = fl.stop_kernel_timing()
+    e_kin = md.kinetic()
+    e_drift = md.E + e_kin - e_tot0
     n_pairs = int(md.pairs.E)
     if a.graphs:
         # HIP events cannot time launches inside graph replays: one more step with every chunk run eagerly, each
@@ -550,6 +553,7 @@ def run_md(a):
                                   "architecture, velocity-Verlet MD dt 0.5 fs, skin 2 A",
                       "atoms": N, "pairs": n_pairs, "chunk": a.chunk, "graphs": a.graphs,
                       "rebuilds_timed": md.n_rebuild - rebuilds0,
+                      "energy_drift_eV": round(e_drift, 6), "kinetic_energy_eV": round(e_kin, 3),
                       "peak_hbm_GB": round(torch.cuda.max_memory_allocated() / 1e9, 2),
                       "box_A": round(float(box[0]), 4)}, roof, kernels, cpu)
     if a.graphs:
