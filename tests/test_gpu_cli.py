@@ -40,6 +40,10 @@ def test_evaluator_on_a_structure_file(tmp_path):
     s.build_neighbors()
     E = ReceiverChunkMACE(mm.MaceModel(seed=0), chunk=96, device="cuda").compute(s)[0]
     assert res["runs"][0]["energy"] == pytest.approx(E, abs=1e-9)
+    # the reference's memory layout and the deterministic mode give the same energy
+    for flags in (["--low-memory"], ["--deterministic"]):
+        r2 = main(["--structure", str(f), "--chunk", "96"] + flags)
+        assert r2["runs"][0]["energy"] == pytest.approx(E, abs=1e-9), flags
 
 
 def test_md_command_line(tmp_path):
