@@ -28,7 +28,8 @@ class ChannelwiseTP:
     """Channelwise TP descriptor: node-feature irreps in_ls (C channels each) x spherical harmonics 0..sh_lmax ->
     mid irreps (l3 in target_ls), e3nn/MACE path order (o3.tp_paths).  The tables of o3.COMPILED_TP_TABLES run
     the library's kernels; any other table with harmonics up to l = 3 runs kernels generated and built for it on
-    first use (tp_jit)."""
+    first use (tp_jit).  The kernels read 16 harmonic components per edge: edge attributes of a table with
+    sh_lmax < 3 ((sh_lmax + 1)^2 components) are zero-padded to 16 on the way in."""
 
     def __init__(self, in_ls, sh_lmax=3, target_ls=(0, 1, 2, 3)):
         self.in_ls, self.sh_lmax, self.target_ls = tuple(in_ls), int(sh_lmax), tuple(target_ls)
@@ -46,8 +47,8 @@ class ChannelwiseTP:
     def kernels(self):
         """(forward, backward) entry points of this table (arguments of mm_tpw_l1_fwd / _bwd): the library's for a
         compiled table, else those built for the table (tp_jit; the first use builds them)."""
-        if self.nY != 16:
-            raise NotImplementedError("the kernels read 16 spherical-harmonic components (l <= 3), "
+        if self.nY > 16:
+            raise NotImplementedError("the kernels take spherical harmonics up to l = 3 (16 components), "
                                       f"not {self.nY} (sh_lmax = {self.sh_lmax})")
         if self.name is not None:
             return getattr(K, f"mm_tpw_{self.name}_fwd"), getattr(K, f"mm_tpw_{self.name}_bwd")
@@ -108,6 +109,8 @@ class _FusedConvFn(torch.autograd.Function):
         E = edge_index.shape[1]
         if Y.shape[0] != E or W.shape[0] != E:
             raise ValueError(f"edge_attrs / tp_weights rows ({Y.shape[0]}, {W.shape[0]}) != number of edges {E}")
+        if desc.nY < 16:                       # the kernels read 16 components; the table uses the first nY
+            Y = torch.nn.functional.pad(Y, (0, 16 - desc.nY))
         n = X.shape[0]
         rowptr, eid, send = receiver_csr(edge_index, n, n)
         out = torch.empty(n, desc.nO * C, dtype=torch.float32, device=X.device)
@@ -134,7 +137,7 @@ class _FusedConvFn(torch.autograd.Function):
                     W.stride(0), gYp, E * 16, gX, X.stride(0), stream())
         gY = None
         if ny:
-            gY = gYp.sum(0) if E else torch.zeros_like(Y)
+            gY = gYp.sum(0)[:, :desc.nY] if E else torch.zeros(0, desc.nY, dtype=Y.dtype, device=Y.device)
         if nw and not E:
             gW = torch.zeros_like(W)
         return gX, gY, gW, None, None

@@ -216,10 +216,11 @@ COMPILED_TP_TABLES = {"l1": ((0,), 3, (0, 1, 2, 3)),
 # Tables without a kernel in the library whose kernels the build makes ahead (mace_onegpu.tp_jit; any other table
 # gets its kernels built on first use): one of each backward layout the generator has besides the compiled
 # tables' -- one channel per lane with two edges in flight (1o input), two path groups (0e+2e input, 145 terms),
-# two channels per lane (0e+1o -> 0e+1o, 21 terms).
+# two channels per lane (0e+1o -> 0e+1o, 21 terms) -- and a table with harmonics up to l = 2 (9 components).
 PREBUILT_JIT_TP_TABLES = (((1,), 3, (0, 1, 2, 3)),
                           ((0, 2), 3, (0, 1, 2, 3)),
-                          ((0, 1), 3, (0, 1)))
+                          ((0, 1), 3, (0, 1)),
+                          ((0, 1), 2, (0, 1, 2)))
 
 
 # ----------------------------------------------------------------------------- symmetric contraction paths

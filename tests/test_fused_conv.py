@@ -36,7 +36,7 @@ def test_module_api_errors():
     m = FusedConvTP(d, 1280, irreps_out="128x0e+128x1o")
     assert m.weight_numel == 1280 and m.irreps_out == "128x0e+128x1o"
     with pytest.raises(NotImplementedError):
-        ChannelwiseTP([0, 1], sh_lmax=2).kernels()         # the kernels read 16 harmonics
+        ChannelwiseTP([0, 1], sh_lmax=4).kernels()         # the kernels take harmonics up to l = 3
     assert "built on first use" in repr(ChannelwiseTP([0, 2]))
 
 
@@ -97,7 +97,7 @@ def test_sparse_table_matches_the_dense_oracle(tab):
     t = o3.tp_table(list(tab[0]), tab[1], tab[2])
     g = np.random.default_rng(3)
     E, Cc = 7, 3
-    W, X, Y = g.normal(size=(E, t["nW"], Cc)), g.normal(size=(E, t["nX"], Cc)), g.normal(size=(E, 16))
+    W, X, Y = g.normal(size=(E, t["nW"], Cc)), g.normal(size=(E, t["nX"], Cc)), g.normal(size=(E, t["nY"]))
     out = np.zeros((E, t["nO"], Cc))
     for (w, k, m, o, c) in t["terms"]:
         out[:, o] += c * W[:, w] * X[:, k] * Y[:, m, None]
@@ -118,7 +118,7 @@ def _oracle(desc, X, Y, W, ei, n):
 def _inputs(desc, n, E, seed, sort):
     g = torch.Generator().manual_seed(seed)
     X = torch.randn(n, desc.nX * C, generator=g, dtype=torch.float64)
-    Y = torch.randn(E, 16, generator=g, dtype=torch.float64)
+    Y = torch.randn(E, desc.nY, generator=g, dtype=torch.float64)
     W = torch.randn(E, desc.nW * C, generator=g, dtype=torch.float64)
     send = torch.randint(0, n, (E,), generator=g)
     recv = torch.randint(0, n - 3, (E,), generator=g)      # the last 3 nodes receive nothing
@@ -180,3 +180,22 @@ def test_fused_conv_bounds_checked_on_host():
         m(X.double(), Y, W, torch.tensor([[0, 1, 2], [0, 1, 2]], device="cuda"))
     out = m(X, Y[:0], W[:0], torch.zeros(2, 0, dtype=torch.long, device="cuda"))
     assert out.shape == (5, desc.nO * C) and float(out.abs().max()) == 0.0
+
+
+@pytest.mark.gpu
+def test_fused_conv_fewer_harmonics_shapes():
+    """A table with harmonics up to l = 2 takes [E, 9] edge attributes (padded to the kernels' 16 inside) and returns
+    a [E, 9] gradient for them, also with no edges; 16 columns are refused for it."""
+    desc = ChannelwiseTP((0, 1), 2, (0, 1, 2))
+    assert desc.nY == 9 and tp_jit.is_current(desc.table)
+    m = FusedConvTP(desc, desc.weight_numel)
+    X = torch.randn(5, desc.nX * C, device="cuda", requires_grad=True)
+    for E in (0, 3):
+        Y = torch.randn(E, 9, device="cuda", requires_grad=True)
+        W = torch.randn(E, desc.weight_numel, device="cuda", requires_grad=True)
+        ei = torch.tensor([[0, 1, 4], [0, 2, 2]], device="cuda")[:, :E]
+        out = m(X, Y, W, ei)
+        gX, gY, gW = torch.autograd.grad(out.sum(), [X, Y, W])
+        assert out.shape == (5, desc.nO * C) and gY.shape == (E, 9) and gW.shape == W.shape
+    with pytest.raises(ValueError):
+        m(X, torch.zeros(3, 16, device="cuda"), torch.zeros(3, desc.weight_numel, device="cuda"), ei)
