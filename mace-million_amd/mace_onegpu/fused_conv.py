@@ -16,6 +16,8 @@ library get theirs built on first use, tp_jit).  Backward (autograd) gives
 d node_feats (atomic adds on senders), d edge_attrs and d tp_weights.  fp32 only, as the reference's fused
 kernels.
 """
+import re
+
 import torch
 
 from . import codegen, o3
@@ -44,6 +46,24 @@ class ChannelwiseTP:
         # the backward kernel returns dL/dY as this many partial rows per edge (one per channel half of a wave)
         self.gy_parts = codegen.tpw_layout(t)["parts"]
 
+    @classmethod
+    def from_irreps(cls, edge_irreps, edge_attrs_irreps, target_irreps):
+        """The descriptor of the reference's path_table(block) (fused_edge_conv.py:43-68) from the block's irreps
+        strings, e3nn notation: node features "128x0e+128x1o" (every irrep 128 channels), edge attributes
+        "1x0e+1x1o+1x2e+1x3o" (the harmonics l = 0 .. L, one copy each) and target irreps "128x0e+128x1o+...".
+        Irreps of the other parity than (-1)^l are not supported (NotImplementedError)."""
+        node, sh, target = (_parse_irreps(x) for x in (edge_irreps, edge_attrs_irreps, target_irreps))
+        for name, irr, mul in (("edge_irreps", node, C), ("target_irreps", target, C), ("edge_attrs_irreps", sh, 1)):
+            for (m, l, p) in irr:
+                if m != mul:
+                    raise ValueError(f"{name}: {m}x{l}{p}, but the kernels take {mul} per irrep")
+                if p != ("e" if l % 2 == 0 else "o"):
+                    raise NotImplementedError(f"{name}: {l}{p} (only the parity (-1)^l of the spherical harmonics)")
+        ls = [l for (_, l, _) in sh]
+        if ls != list(range(len(ls))):
+            raise ValueError(f"edge_attrs_irreps must be the harmonics l = 0 .. L in order, not {edge_attrs_irreps!r}")
+        return cls([l for (_, l, _) in node], len(ls) - 1, tuple(l for (_, l, _) in target))
+
     def kernels(self):
         """(forward, backward) entry points of this table (arguments of mm_tpw_l1_fwd / _bwd): the library's for a
         compiled table, else those built for the table (tp_jit; the first use builds them)."""
@@ -59,6 +79,17 @@ class ChannelwiseTP:
         kern = self.name if self.name is not None else "built on first use"
         return (f"ChannelwiseTP(in_ls={self.in_ls}, sh_lmax={self.sh_lmax}, target_ls={self.target_ls}; nX={self.nX}, "
                 f"nW={self.nW}, nO={self.nO}, terms={len(self.table['terms'])}, kernel={kern})")
+
+
+def _parse_irreps(text):
+    """[(multiplicity, l, parity)] of an e3nn irreps string such as "128x0e+128x1o" (a bare "1o" means 1x1o)."""
+    out = []
+    for part in str(text).replace(" ", "").split("+"):
+        m = re.fullmatch(r"(?:(\d+)x)?(\d+)([eo])", part)
+        if not m:
+            raise ValueError(f"cannot read irreps {text!r} (at {part!r})")
+        out.append((int(m.group(1) or 1), int(m.group(2)), m.group(3)))
+    return out
 
 
 def receiver_csr(edge_index, n_nodes, n_send_rows):

@@ -40,6 +40,23 @@ def test_module_api_errors():
     assert "built on first use" in repr(ChannelwiseTP([0, 2]))
 
 
+def test_descriptor_from_irreps_strings():
+    """The irreps strings of a MACE interaction block (what the reference's path_table reads) give the same
+    descriptor as the l lists; multiplicities other than the kernels' and pseudo-parities are refused."""
+    d = ChannelwiseTP.from_irreps("128x0e+128x1o", "1x0e+1x1o+1x2e+1x3o", "128x0e+128x1o+128x2e+128x3o")
+    assert (d.in_ls, d.sh_lmax, d.target_ls, d.name) == ((0, 1), 3, (0, 1, 2, 3), "l2")
+    d = ChannelwiseTP.from_irreps("128x0e", "0e+1o+2e", "128x0e + 128x2e")
+    assert (d.in_ls, d.sh_lmax, d.target_ls, d.nY) == ((0,), 2, (0, 2), 9)
+    with pytest.raises(ValueError, match="128 per irrep"):
+        ChannelwiseTP.from_irreps("64x0e", "1x0e", "128x0e")
+    with pytest.raises(NotImplementedError, match="parity"):
+        ChannelwiseTP.from_irreps("128x1e", "1x0e+1x1o", "128x0e")
+    with pytest.raises(ValueError, match="l = 0 .. L"):
+        ChannelwiseTP.from_irreps("128x0e", "1x0e+1x2e", "128x0e")
+    with pytest.raises(ValueError, match="cannot read"):
+        ChannelwiseTP.from_irreps("128x0y", "1x0e", "128x0e")
+
+
 def test_run_time_tables_are_prebuilt_and_export_their_entry_points():
     """The build makes the kernels of o3.PREBUILT_JIT_TP_TABLES ahead, from this tree's sources; their libraries
     load without a GPU and export both entry points under the table's name."""
