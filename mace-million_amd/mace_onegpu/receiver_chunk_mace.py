@@ -275,6 +275,16 @@ class ReceiverChunkMACE:
         gx.begin(graphs)
         return gx
 
+    def _idle_exec(self, sysm):
+        """The graph executor of an earlier call, for its static H1 / G1 / layer-1 cache rows, when they hold this
+        system (same box, at most nt_cap atoms, the same layer-1 cache setting); else None."""
+        gx = self._gx
+        if gx is None or gx.box != tuple(float(b) for b in sysm.box) or sysm.N > gx.nt_cap:
+            return None
+        if gx.cache_layer1 != self.cache_layer1:
+            return None
+        return gx
+
     def _compute_low_memory(self, sysm, timings):
         """The three passes with each chunk's topology rebuilt when a pass reaches it and its pair forces added to
         F at once (low_memory); returns (E, eat, F, None)."""
@@ -329,13 +339,16 @@ class ReceiverChunkMACE:
         sync()
         t0 = time.perf_counter()
         gx = self._graph_exec(fl, sysm, graphs) if self.use_graphs else None
+        # without graphs for this call, an executor of an earlier call whose static rows hold this system lends
+        # them, instead of a second set of H1, G1 and layer-1 cache rows
+        bx = gx if gx is not None else self._idle_exec(sysm)
         nC = self.chunk
         cache = None
         # pass A writes every column of every receiver's h1 row, and pass B stores every pair force of its chunk
         # before pass C adds to it: neither buffer is cleared first (G1 and eat are accumulated into and are)
-        if gx is not None:      # the executor's static buffers: its graphs read and write them in place
-            H1, G1, eat = gx.H1x[:N], gx.G1[:N], gx.eat[:N]
-            cache = gx.cache()
+        if bx is not None:      # the executor's static buffers: its graphs read and write them in place
+            H1, G1, eat = bx.H1x[:N], bx.G1[:N], bx.eat[:N]
+            cache = bx.cache()
         else:
             H1 = torch.empty(N, self.D1, dtype=torch.float32, device=dev)
             if self.cache_layer1:
@@ -350,7 +363,7 @@ class ReceiverChunkMACE:
         sync()
         t["A"] = time.perf_counter() - t0
         t0 = time.perf_counter()
-        if gx is not None:
+        if bx is not None:
             G1.zero_()
             eat.zero_()
         else:
