@@ -128,6 +128,9 @@ class ChunkGraphExec:
         self.ws = None
         self.n_replays = 0
         self.n_captured = 0
+        # one memory pool for the graphs of every slot: a replay's temporaries are dead when it ends and replays
+        # never overlap (one stream), so graphs of different slots can share the pool's blocks
+        self.pool = None
 
     def cache(self):
         return dict(M=self.M, rho=self.rho) if self.cache_layer1 else None
@@ -274,11 +277,12 @@ class ChunkGraphExec:
                     fn(s)
             torch.cuda.current_stream().wait_stream(side)
             torch.cuda.synchronize()
-            pool = torch.cuda.graph_pool_handle()
+            if self.pool is None:
+                self.pool = torch.cuda.graph_pool_handle()
             graphs = {}
             for name, fn in bodies:
                 gr = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(gr, pool=pool):
+                with torch.cuda.graph(gr, pool=self.pool):
                     fn(s)
                 graphs[name] = gr
             torch.cuda.synchronize()

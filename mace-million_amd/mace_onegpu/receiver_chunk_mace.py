@@ -342,6 +342,10 @@ class ReceiverChunkMACE:
         # without graphs for this call, an executor of an earlier call whose static rows hold this system lends
         # them, instead of a second set of H1, G1 and layer-1 cache rows
         bx = gx if gx is not None else self._idle_exec(sysm)
+        if bx is not None and bx.ws is not None:
+            # the executor's workspace (sized for its capacities) serves the eager chunks too: a partial chunk,
+            # or every chunk of a call without graphs, instead of a second workspace
+            fl.ws = bx.ws
         nC = self.chunk
         cache = None
         # pass A writes every column of every receiver's h1 row, and pass B stores every pair force of its chunk

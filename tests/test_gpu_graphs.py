@@ -109,11 +109,13 @@ def test_standalone_graphs_match_eager(model, water_sys):
         torch.cuda.synchronize()
         _close(E1, PF1, eat1, E0, PF0, eat0, s.N, f"call {call}")
     assert ev1.n_captures == 1 and ev1._gx.n_replays == 27
-    # an eager call of the same evaluator runs on the executor's static rows (no second set of H1, G1 and
-    # layer-1 cache rows) and still equals the eager evaluator; a graph call after it is unaffected
+    # an eager call of the same evaluator runs on the executor's static rows and workspace (no second set of H1,
+    # G1, layer-1 cache rows and chunk buffers) and still equals the eager evaluator; a graph call after it is
+    # unaffected
     ev1.use_graphs = False
     E2, eat2, F2, PF2 = ev1.compute(s)
     assert ev1.H1.data_ptr() == ev1._gx.H1x.data_ptr() and ev1.G1.data_ptr() == ev1._gx.G1.data_ptr()
+    assert ev1.fl.ws is ev1._gx.ws                                 # and its workspace
     E0, eat0, F0, PF0 = ev0.compute(s)
     _close(E2, PF2, eat2, E0, PF0, eat0, s.N, "eager call on the executor's rows")
     ev1.use_graphs = True
