@@ -306,6 +306,8 @@ class _Runtime:
         stamp = _Stamps(timings)
         chunks = self.chunks(batch, elems, nl, nt)
         gx = self.graph_executor(chunks, nt)
+        if gx is not None and gx.ws is not None:
+            self.fl.ws = gx.ws          # the executor's capacity-sized workspace serves the partial chunk too
         call = _CallBuffers(self, nl, nt, P, gx)
         eager = _EagerPasses(self.fl, call)
         run = [gx if gx is not None and g.nC == self.chunk else eager for g in chunks]
