@@ -354,7 +354,10 @@ class FastLayers:
                   e_recv=torch.empty(E, **i), e_dd=torch.empty(E, **f), part=torch.empty(NCB * E * 17, **f))
         if self.deterministic:
             ws["gXe"] = torch.empty(E, 4 * C, **f)       # per-edge dL/dX rows of mm_conv2_bwd_det
-        ws.update(A=torch.empty(nC * self.nO2 * C, **f), gA=torch.empty(nC * self.nO2 * C, **f),
+        # A (a layer's message, read by the linear after its convolution) and gA (its cotangent, written by the
+        # transposed linear and read by the backward convolution) are never live together in a pass: one buffer
+        A = torch.empty(nC * self.nO2 * C, **f)
+        ws.update(A=A, gA=A,
                   rho=torch.empty(nC, **f), g_rho=torch.empty(nC, **f),
                   M=torch.empty(nC * 16 * C, **f), gM=torch.empty(nC * 16 * C, **f),
                   B=torch.empty(nC * 4 * C, **f), gB=torch.empty(nC * 4 * C, **f),
