@@ -41,9 +41,12 @@ def _align(x, a):
     return ((int(x) + a - 1) // a) * a
 
 
-def capacities(n_max, e_max, nt, e_align=65536, margin=1.25):
-    """(n_cap, e_cap, nt_cap) with the reference's headroom (mliap_threepass.py:418-421)."""
-    return _align(int(n_max * margin) + 2, 1024), _align(int(e_max * margin), e_align), int(nt * margin) + 1024
+def capacities(n_max, e_max, nt, e_align=65536, margin=1.25, nt_margin=None):
+    """(n_cap, e_cap, nt_cap) with the reference's headroom (mliap_threepass.py:418-421).  nt_margin (default:
+    margin) is the headroom of the atom rows: LAMMPS' ghost count changes between calls, a standalone system's
+    atom count does not."""
+    ntm = margin if nt_margin is None else nt_margin
+    return _align(int(n_max * margin) + 2, 1024), _align(int(e_max * margin), e_align), int(nt * ntm) + 1024
 
 
 class _Slot:

@@ -265,7 +265,8 @@ class ReceiverChunkMACE:
         if gx is None or gx.box != box or not gx.fits(n_max, e_max, sysm.N):
             self._gx = gx = None
             torch.cuda.empty_cache()
-            n_cap, e_cap, nt_cap = chunk_graphs.capacities(n_max, e_max, sysm.N, self.e_align)
+            # the chunks' nodes and edges change as atoms move (25 % headroom); the atom count of a System does not
+            n_cap, e_cap, nt_cap = chunk_graphs.capacities(n_max, e_max, sysm.N, self.e_align, nt_margin=1.0)
             gx = chunk_graphs.ChunkGraphExec(fl, self.chunk, n_cap, e_cap, nt_cap, "pos", self.cache_layer1,
                                              box_host=host_f64(box))
             gx.box = box

@@ -124,3 +124,12 @@ def test_reload_copies_the_node_set_only_when_it_changed():
     assert torch.equal(s.nodes[:h.n_nodes], h.nodes) and bool((s.nodes[h.n_nodes:] == ex.sink).all())
     assert torch.equal(s.ls[:h.nE], h.ls)
     ex.check(s)
+
+
+def test_capacities_headroom():
+    """25 % headroom on chunk nodes and edges (aligned), and on the atom rows unless nt_margin says otherwise (a
+    standalone system keeps its atom count)."""
+    from mace_onegpu import chunk_graphs
+    n_cap, e_cap, nt_cap = chunk_graphs.capacities(1000, 100000, 5000, 65536, 1.25)
+    assert n_cap == 2048 and e_cap == 131072 and nt_cap == 6250 + 1024
+    assert chunk_graphs.capacities(1000, 100000, 5000, 65536, 1.25, nt_margin=1.0) == (2048, 131072, 6024)
