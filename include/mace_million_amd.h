@@ -65,6 +65,11 @@ int mm_nl_filter_fill(const double* pos, long N, const double* box /* HOST [3] *
                       const int* skin_send, double r_max2, const long* rowptr, int* send,
                       int* filtered_index /* nullable: per skin pair, its index in the filtered list or -1 */,
                       int from_flags, mm_stream_t stream);
+/* rev[e] = the index of the pair (j, i) for every pair e = (i, j) of a symmetric CSR list of E pairs (the skin
+ * list's reverse-pair map that mm_pair_forces_skin reads; no counterpart in the reference, whose MD runs inside
+ * LAMMPS).  rev is filled by the caller (e.g. with -1): a pair without a reverse keeps that value.  E < 2^31
+ * (else MM_ERANGE). */
+int mm_nl_reverse(const long* rowptr, const int* send, long N, long E, int* rev, mm_stream_t stream);
 
 /* ---------------------------------------------------------------------------------------------- edge geometry
  * Replace receiver_chunk_mace.edge_embed (:230-234), the table coordinates of spline_w._coords (spline_w.py:18-27)

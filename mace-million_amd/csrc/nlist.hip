@@ -454,3 +454,52 @@ extern "C" int mm_nl_filter_fill(const double* pos, long N, const double* box, c
                        N, box[0], box[1], box[2], rp_s, send_s, r2, (int*)nullptr, rowptr, send, fidx);
   return mm::launch_status("mm_nl_filter_fill");
 }
+
+// rev[e] = index of the pair (j, i) for every pair e = (i, j) of a symmetric CSR pair list (the MD driver's skin
+// list), found by scanning row j; no sort and no memory beyond rev.  One wave per receiver i: the senders of 64 of
+// its pairs and the bounds of their rows are loaded together, then each 16-lane quarter of the wave searches one
+// pair's row, 256 candidates per round (16 loads per lane in flight).  Every sender occurs at most once in a row
+// (one minimum image), so at most one lane writes each rev[e]; a pair without a reverse keeps the caller's fill.
+__global__ void __launch_bounds__(256) mm_nl_reverse_kernel(long N, const long* __restrict__ rowptr,
+                                                            const int* __restrict__ send, int* __restrict__ rev) {
+  const long i = blockIdx.x * 4L + (threadIdx.x >> 6);
+  if (i >= N) return;
+  const int lane = threadIdx.x & 63, q = lane >> 4, lq = lane & 15;
+  const long b0 = rowptr[i], b1 = rowptr[i + 1];
+  for (long eb = b0; eb < b1; eb += 64) {
+    // lanes past the row hold an empty range [0, 0)
+    int s0 = 0, len = 0;
+    if (eb + lane < b1) {
+      const int j = send[eb + lane];
+      s0 = (int)rowptr[j];
+      len = (int)(rowptr[j + 1] - s0);
+    }
+    const int n = (int)min(64L, b1 - eb);
+    for (int k = 0; k < n; k += 4) {
+      const int src = k + q;                       // the pair this quarter searches: eb + src
+      const int c0 = __shfl(s0, src), cl = __shfl(len, src);
+      for (int c = 0; c < cl; c += 256) {
+        int v[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+          const int x = c + 16 * t + lq;
+          v[t] = x < cl ? send[c0 + x] : -1;
+        }
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+          if (v[t] == (int)i) rev[eb + src] = c0 + c + 16 * t + lq;
+      }
+    }
+  }
+}
+
+extern "C" int mm_nl_reverse(const long* rowptr, const int* send, long N, long E, int* rev, hipStream_t stream) {
+  MM_CHECK_ARG(N >= 0 && E >= 0 && (N == 0 || (rowptr && send && rev)), "bad arguments");
+  if (E > 2147483647L) {
+    mm::set_error("mm_nl_reverse: " + std::to_string(E) + " pairs exceed the int32 pair index");
+    return MM_ERANGE;
+  }
+  if (N == 0 || E == 0) return MM_OK;
+  hipLaunchKernelGGL(mm_nl_reverse_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, N, rowptr, send, rev);
+  return mm::launch_status("mm_nl_reverse");
+}

@@ -37,6 +37,7 @@ SIGNATURES = {
     "mm_nl_fill": [P, P, L, P, P, P, P, D, I, P, P, P],
     "mm_nl_filter_count": [P, L, P, P, P, D, P, P, P],
     "mm_nl_filter_fill": [P, L, P, P, P, D, P, P, P, I, P],
+    "mm_nl_reverse": [P, P, L, L, P, P],
     # geometry
     "mm_edge_geom_rij": [I, P, P, P, I, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],
     "mm_edge_geom_pos": [I, P, P, P, P, I, P, P, P, I, P, P, I, F, I, I, F, F, I, P, P, P, P, P, P],

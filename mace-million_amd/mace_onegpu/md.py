@@ -111,19 +111,14 @@ class PairList:
 
 def reverse_pairs(sysm):
     """rev[e] = index of the pair (j, i) for every pair e = (i, j) of a symmetric CSR neighbour list (the cell-list
-    test is symmetric bit for bit: d(j, i) = -d(i, j) exactly in fp64)."""
-    N = sysm.N
-    dev = sysm.send.device
-    recv = torch.repeat_interleave(torch.arange(N, device=dev, dtype=torch.int64), sysm.NN.long())
-    send = sysm.send.long()
-    key = recv * N + send
-    order = torch.argsort(key)
-    skey = key[order]
-    rkey = send * N + recv
-    pos = torch.searchsorted(skey, rkey).clamp_(max=max(skey.numel() - 1, 0))
-    if skey.numel() and not bool((skey[pos] == rkey).all()):
+    test is symmetric bit for bit: d(j, i) = -d(i, j) exactly in fp64), by mm_nl_reverse: each pair's reverse is
+    found by scanning the sender's row, so the map needs no memory beyond its own int32 per pair."""
+    E = int(sysm.send.numel())
+    rev = torch.full((max(E, 1),), -1, dtype=torch.int32, device=sysm.send.device)
+    K.mm_nl_reverse(sysm.rowptr, sysm.send, sysm.N, E, rev, stream())
+    if E and int(rev[:E].min()) < 0:
         raise RuntimeError("neighbour list is not symmetric")
-    return order[pos].to(torch.int32)
+    return rev
 
 
 class MDRunner:
@@ -150,6 +145,8 @@ class MDRunner:
         self.eat = None
 
     def _build(self, pos):
+        # the previous lists go first: the new skin list is then built in their memory
+        self.pairs = self.skin_sys = None
         spidx = (self.Z - 1).to(torch.int32)
         s = System(pos, self.box, spidx, self.r_max + self.skin, device=self.dev)
         perm = s.perm

@@ -104,21 +104,68 @@ def test_product_chunk_topology_matches_reference(ci):
     assert bool((loc == -1).all()) and not bool(flag.any())
 
 
+def _reverse_by_sort(rp, send):
+    """The reverse-pair map by sorting the pairs by (receiver, sender) (numpy)."""
+    N = len(rp) - 1
+    recv = np.repeat(np.arange(N, dtype=np.int64), np.diff(rp))
+    key = recv * N + send
+    order = np.argsort(key, kind="stable")
+    pos = np.searchsorted(key[order], send.astype(np.int64) * N + recv)
+    return order[pos]
+
+
+def _random_symmetric(N, p, seed):
+    """A symmetric pair list with every row in a random order (rows of 0 to about p N pairs)."""
+    rng = np.random.default_rng(seed)
+    adj = np.triu(rng.random((N, N)) < p, 1)
+    adj |= adj.T
+    rows = [rng.permutation(np.flatnonzero(adj[i])) for i in range(N)]
+    rp = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int64)
+    return rp, np.concatenate(rows).astype(np.int32)
+
+
+@pytest.mark.gpu
 def test_reverse_pairs_map():
-    """reverse_pairs (the MD force sum's reverse-pair map) is an involution mapping (i, j) to (j, i)."""
+    """reverse_pairs (mm_nl_reverse, the MD force sum's reverse-pair map) maps (i, j) to (j, i), equal to the map
+    found by sorting: on the cell list of the golden water box (rows of about 90 pairs in candidate order), on a
+    complete graph (rows of 599 pairs: three 256-candidate rounds, ten 64-pair blocks) and on a random graph with
+    rows of 0 to 400 pairs; a list without a reverse pair raises."""
     import torch
     from mace_onegpu.md import reverse_pairs
 
+    assert torch.cuda.is_available(), "GPU test without a GPU"
     g = golden("water648_cells")
     s = neighbors.SystemRef(g["pos"], g["box"], g["spidx"], 6.0)
     NN, rp, send = s.build_neighbors()
+    n = 600
+    full = np.array([np.random.default_rng(i).permutation(np.delete(np.arange(n), i)) for i in range(n)]).ravel()
+    cases = [(np.asarray(rp, np.int64), np.asarray(send, np.int32)),
+             (np.arange(n + 1, dtype=np.int64) * (n - 1), full.astype(np.int32)),
+             _random_symmetric(1000, 0.4, 3), _random_symmetric(700, 0.02, 4)]
 
     class V:
         pass
+    for rp_c, send_c in cases:
+        v = V()
+        v.N = len(rp_c) - 1
+        v.rowptr = torch.as_tensor(rp_c, device="cuda")
+        v.send = torch.as_tensor(send_c, device="cuda")
+        rev = reverse_pairs(v).cpu().numpy().astype(np.int64)
+        assert np.array_equal(rev, _reverse_by_sort(rp_c, send_c)), v.N
+        assert np.array_equal(rev[rev], np.arange(len(send_c)))
     v = V()
-    v.N, v.NN, v.send = s.N, torch.as_tensor(NN), torch.as_tensor(send)
-    rev = reverse_pairs(v).long()
-    recv = torch.repeat_interleave(torch.arange(s.N), v.NN.long())
-    e = torch.arange(len(send))
-    assert torch.equal(rev[rev], e)
-    assert torch.equal(recv[rev], v.send.long()) and torch.equal(v.send.long()[rev], recv)
+    v.N, v.rowptr = 2, torch.tensor([0, 1, 1], device="cuda")
+    v.send = torch.tensor([1], dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="not symmetric"):
+        reverse_pairs(v)
+
+
+def test_reverse_map_by_sort_is_an_involution():
+    """The sorting restatement that the GPU map is checked against: (i, j) -> (j, i) on the golden water box."""
+    g = golden("water648_cells")
+    s = neighbors.SystemRef(g["pos"], g["box"], g["spidx"], 6.0)
+    NN, rp, send = s.build_neighbors()
+    rev = _reverse_by_sort(np.asarray(rp, np.int64), np.asarray(send, np.int64))
+    recv = np.repeat(np.arange(s.N), NN)
+    assert np.array_equal(rev[rev], np.arange(len(send)))
+    assert np.array_equal(recv[rev], send) and np.array_equal(np.asarray(send)[rev], recv)
