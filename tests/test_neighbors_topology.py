@@ -124,6 +124,55 @@ def _random_symmetric(N, p, seed):
     return rp, np.concatenate(rows).astype(np.int32)
 
 
+def _random_pairs(nl, nt, kmax, seed, self_pairs):
+    """Receivers 0..nl-1 in order with random degrees 0..kmax (one receiver without pairs when nl > 3), senders
+    anywhere in 0..nt-1 (nt > nl: ghosts); without self_pairs a sender equal to its receiver is moved to the next
+    atom."""
+    rng = np.random.default_rng(seed)
+    deg = rng.integers(0, kmax + 1, size=nl)
+    if nl > 3:
+        deg[rng.integers(0, nl)] = 0
+    pi = np.repeat(np.arange(nl), deg).astype(np.int32)
+    pj = rng.integers(0, nt, size=pi.size).astype(np.int32)
+    if not self_pairs:
+        same = pj == pi
+        pj[same] = (pj[same] + 1) % nt
+    return pi, pj
+
+
+# the pair-list shapes of the reference's tests/test_topology.py:40-51 (nl, nt, chunk, kmax, seed, self pairs)
+TOPO_CASES = [(1000, 1300, 128, 12, 0, False), (1000, 1300, 1000, 12, 1, False), (1000, 1000, 4096, 12, 2, False),
+              (1000, 1000, 100, 12, 3, False), (777, 901, 64, 30, 4, False), (5, 9, 2, 3, 5, False),
+              (1, 4, 16, 3, 6, False), (3000, 3400, 256, 8, 7, True), (20000, 23000, 2048, 20, 8, False)]
+
+
+@pytest.mark.parametrize("nl,nt,C,kmax,seed,self_pairs", TOPO_CASES)
+def test_product_chunk_topology_on_random_pair_lists(nl, nt, C, kmax, seed, self_pairs):
+    """The product's chunk builder equals the oracle's topology (pinned on the golden vectors above) on the
+    reference's pair-list shapes: ghosts, a partial last chunk, one chunk with or without ghosts, chunks larger
+    than the receiver count, a single local atom, pairs i == i, receivers without pairs."""
+    import torch
+    from mace_onegpu.receiver_chunk_mace import chunk_topology
+    pi, pj = _random_pairs(nl, nt, kmax, seed, self_pairs)
+    rp = np.searchsorted(pi, np.arange(nl + 1))
+    pj_t = torch.as_tensor(pj)
+    loc = torch.full((nt,), -1, dtype=torch.int32)
+    flag = torch.zeros(nt, dtype=torch.bool)
+    for a in range(0, nl, C):
+        b = min(a + C, nl)
+        e0, e1 = int(rp[a]), int(rp[b])
+        nodes, ls = chunk_topology(a, b, e0, e1, pj_t, loc, flag)
+        nodes_o, ls_o = topology.topology(a, b, pi[e0:e1], pj[e0:e1])
+        assert nodes.dtype == torch.int32 and ls.dtype == torch.int32
+        assert np.array_equal(nodes.numpy(), nodes_o) and np.array_equal(ls.numpy(), ls_o), (a, b)
+        n = nodes.numpy().astype(np.int64)
+        assert np.array_equal(n[ls.numpy()], pj[e0:e1]) and np.array_equal(n[pi[e0:e1] - a], pi[e0:e1])
+        assert np.array_equal(n[:b - a], np.arange(a, b))                      # receivers first
+        out = n[b - a:]
+        assert np.all(np.diff(out) > 0) and not np.any((out >= a) & (out < b))  # then outside senders, ascending
+    assert bool((loc == -1).all()) and not bool(flag.any())
+
+
 @pytest.mark.gpu
 def test_reverse_pairs_map():
     """reverse_pairs (mm_nl_reverse, the MD force sum's reverse-pair map) maps (i, j) to (j, i), equal to the map
